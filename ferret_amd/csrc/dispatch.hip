@@ -1,0 +1,61 @@
+// Library-level entry points: version / error text, workspace sizing, and the
+// shape dispatch between the skinny (<= 16 token) streaming kernels and the
+// tiled MFMA kernels.
+#include "common.hpp"
+
+int ferret_fp8_gemm_skinny(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
+                           int N, int K, hipStream_t st);
+int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
+                          int N, int K, hipStream_t st);
+int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, const float* sw,
+                              const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                              int max_tiles, int topk, int N, int K, void* out, hipStream_t st);
+int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, const float* sw,
+                             const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                             int max_tiles, int topk, int N, int K, void* out, hipStream_t st);
+
+extern "C" const char* ferret_version(void) { return "ferret-hip 0.1.0 gfx950"; }
+
+extern "C" const char* ferret_error_string(int code) {
+  switch (code) {
+    case FERRET_OK: return "ok";
+    case FERRET_ERR_NULL: return "a required pointer is NULL";
+    case FERRET_ERR_SHAPE: return "sizes out of range or not supported";
+    case FERRET_ERR_WORKSPACE: return "workspace missing or too small";
+    default: break;
+  }
+  return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown ferret error";
+}
+
+extern "C" size_t ferret_workspace_bytes(int op, int M, int N, int K, int E) {
+  (void)op; (void)M; (void)N; (void)K; (void)E;
+  return 0;
+}
+
+extern "C" int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, const float* sb,
+                                          void* c, int M, int N, int K, void* ws, size_t ws_bytes,
+                                          void* stream) {
+  (void)ws; (void)ws_bytes;
+  FERRET_REQUIRE(a && sa && b && sb && c, FERRET_ERR_NULL);
+  FERRET_REQUIRE(M >= 1 && N >= 16 && K >= 128 && N % 16 == 0 && K % 128 == 0 && K / 128 <= 128,
+                 FERRET_ERR_SHAPE);
+  if (M <= 16) return ferret_fp8_gemm_skinny(a, sa, b, sb, c, M, N, K, (hipStream_t)stream);
+  FERRET_REQUIRE(N % 128 == 0, FERRET_ERR_SHAPE);
+  return ferret_fp8_gemm_tiled(a, sa, b, sb, c, M, N, K, (hipStream_t)stream);
+}
+
+extern "C" int ferret_moe_w13_fp8(const void* x, const float* sx, const void* w, const float* sw,
+                                  const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                                  int max_tiles, int tile_m, int T, int topk, int E, int N, int K, void* out,
+                                  void* stream) {
+  FERRET_REQUIRE(x && sx && w && sw && sorted_pair && tiles && ntiles && out, FERRET_ERR_NULL);
+  FERRET_REQUIRE(T >= 1 && topk >= 1 && E >= 1 && max_tiles >= 0, FERRET_ERR_SHAPE);
+  FERRET_REQUIRE(N % 256 == 0 && K % 128 == 0 && K >= 128 && K / 128 <= 128, FERRET_ERR_SHAPE);
+  if (tile_m == 16)
+    return ferret_moe_w13_fp8_skinny(x, sx, w, sw, sorted_pair, tiles, ntiles, max_tiles, topk, N, K, out,
+                                     (hipStream_t)stream);
+  if (tile_m == 128)
+    return ferret_moe_w13_fp8_tiled(x, sx, w, sw, sorted_pair, tiles, ntiles, max_tiles, topk, N, K, out,
+                                    (hipStream_t)stream);
+  return FERRET_ERR_SHAPE;
+}

@@ -1,0 +1,164 @@
+"""PyTorch-facing wrappers over the C ABI (device tensors in, device tensors out).
+
+Every wrapper validates dtype / device / contiguity / shape on the host, passes
+raw device pointers plus the current HIP stream, and raises FerretError on a
+non-zero return code.  There is no CPU path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import lib as _lib
+
+FP8 = torch.float8_e4m3fn
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None) -> int:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device}); ferret_amd has no CPU path")
+    if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise TypeError(f"{name} must have dtype {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def linear_bf16(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M,N] = x[M,K] @ w[N,K]^T (+ residual), bf16 in/out, fp32 accumulate."""
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    rp = 0
+    if residual is not None:
+        if tuple(residual.shape) != (M, N):
+            raise ValueError("residual must be [M, N]")
+        rp = _dev(residual, "residual", torch.bfloat16)
+    rc = _lib.load().ferret_linear_bf16(_dev(x, "x", torch.bfloat16, 2), _dev(w, "w", torch.bfloat16, 2), rp,
+                                        _dev(out, "out", torch.bfloat16, 2), M, N, K, None, 0, _stream())
+    _lib.check("ferret_linear_bf16", rc)
+    return out
+
+
+def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """c[M,N] (bf16) = block-scaled a[M,K] (e4m3) . b[N,K]^T (e4m3)."""
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError("b must be [N, K]")
+    if tuple(sa.shape) != (M, K // 128) or tuple(sb.shape) != ((N + 127) // 128, K // 128):
+        raise ValueError(f"scale shapes must be sa [M, K/128], sb [ceil(N/128), K/128]; got {tuple(sa.shape)}, {tuple(sb.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    rc = _lib.load().ferret_fp8_gemm_blockscale(
+        _dev(a, "a", (FP8, torch.uint8), 2), _dev(sa, "sa", torch.float32, 2), _dev(b, "b", (FP8, torch.uint8), 2),
+        _dev(sb, "sb", torch.float32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K, None, 0, _stream())
+    _lib.check("ferret_fp8_gemm_blockscale", rc)
+    return out
+
+
+def moe_route_topk(logits: torch.Tensor, topk: int, with_weights: bool = True):
+    """ids int32 [T, topk] (logit desc, expert asc) and softmax weights [T, topk]."""
+    T, E = logits.shape
+    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device) if with_weights else None
+    rc = _lib.load().ferret_moe_route_topk(_dev(logits, "logits", torch.float32, 2), T, E, topk,
+                                           _dev(ids, "ids"), w.data_ptr() if w is not None else 0, _stream())
+    _lib.check("ferret_moe_route_topk", rc)
+    return ids, w
+
+
+@dataclass
+class Routing:
+    """Device tensors describing how routed pairs are grouped by expert."""
+    counts: torch.Tensor        # int32 [E]
+    offsets: torch.Tensor       # int32 [E+1]
+    sorted_pair: torch.Tensor   # int32 [P]
+    tiles: torch.Tensor         # int32 [max_tiles, 3]
+    ntiles: torch.Tensor        # int32 [1]
+    tile_m: int
+    max_tiles: int
+    num_experts: int
+    topk: int
+    num_tokens: int
+
+
+def tile_m_for(num_pairs: int, num_experts: int) -> int:
+    return int(_lib.load().ferret_moe_tile_m(num_pairs, num_experts))
+
+
+def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int | None = None) -> Routing:
+    T, topk = ids.shape
+    P = T * topk
+    if tile_m is None:
+        tile_m = tile_m_for(P, num_experts)
+    L = _lib.load()
+    max_tiles = max(1, int(L.ferret_moe_max_tiles(P, num_experts, tile_m)))
+    dev = ids.device
+    r = Routing(
+        counts=torch.empty(num_experts, dtype=torch.int32, device=dev),
+        offsets=torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        sorted_pair=torch.empty(max(P, 1), dtype=torch.int32, device=dev),
+        tiles=torch.empty((max_tiles, 3), dtype=torch.int32, device=dev),
+        ntiles=torch.empty(1, dtype=torch.int32, device=dev),
+        tile_m=tile_m, max_tiles=max_tiles, num_experts=num_experts, topk=topk, num_tokens=T)
+    rc = L.ferret_moe_permute(_dev(ids, "ids", torch.int32, 2), T, topk, num_experts, tile_m,
+                              r.counts.data_ptr(), r.offsets.data_ptr(), r.sorted_pair.data_ptr(),
+                              r.tiles.data_ptr(), max_tiles, r.ntiles.data_ptr(), _stream())
+    _lib.check("ferret_moe_permute", rc)
+    return r
+
+
+def moe_w13_fp8(x: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, routing: Routing,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[P, N/2] bf16 = silu(gate) * up of the FP8 block-scaled w13 projection."""
+    T, K = x.shape
+    E, N, K2 = w.shape
+    if K2 != K or E != routing.num_experts or T != routing.num_tokens:
+        raise ValueError("shape mismatch between x, w and routing")
+    if tuple(sx.shape) != (T, K // 128) or tuple(sw.shape) != (E, N // 128, K // 128):
+        raise ValueError("scale shapes must be sx [T, K/128], sw [E, N/128, K/128]")
+    P = T * routing.topk
+    if out is None:
+        out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
+    rc = _lib.load().ferret_moe_w13_fp8(
+        _dev(x, "x", (FP8, torch.uint8), 2), _dev(sx, "sx", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
+        _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
+        routing.ntiles.data_ptr(), routing.max_tiles, routing.tile_m, T, routing.topk, E, N, K,
+        _dev(out, "out", torch.bfloat16, 2), _stream())
+    _lib.check("ferret_moe_w13_fp8", rc)
+    return out
+
+
+def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: Routing,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[P, N/2] bf16 = silu(gate) * up of the INT4 W4A16 w13 projection."""
+    T, K = x.shape
+    E, N, K8 = wq.shape
+    if K8 * 8 != K or E != routing.num_experts or T != routing.num_tokens:
+        raise ValueError("shape mismatch between x, wq and routing")
+    if tuple(ws.shape) != (E, N, K // 32):
+        raise ValueError("ws must be [E, N, K/32] bf16")
+    P = T * routing.topk
+    if out is None:
+        out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
+    rc = _lib.load().ferret_moe_w13_w4a16(
+        _dev(x, "x", torch.bfloat16, 2), _dev(wq, "wq", torch.int32, 3), _dev(ws, "ws", torch.bfloat16, 3),
+        routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(), routing.ntiles.data_ptr(), routing.max_tiles,
+        routing.tile_m, T, routing.topk, E, N, K, _dev(out, "out", torch.bfloat16, 2), _stream())
+    _lib.check("ferret_moe_w13_w4a16", rc)
+    return out

@@ -1,0 +1,167 @@
+"""The benchmark configurations of the quantized-GEMM path and their seeded inputs.
+
+Seven workloads (the four math cases at their DeepSeek-V3 / Qwen3-8B / Kimi-K2
+shapes).  Inputs are generated with torch on any device from per-tensor seeds;
+the quantizer below is the build's absmax/448 rule (1x128 activation blocks,
+128x128 weight blocks, fp32 scales), the same rule DeepGEMM's
+per_token_cast_to_fp8 / per_block_cast_to_fp8 implement at the reference's call
+sites (baselines/fp8-gemm/baseline_prefill.py:41-42,
+baselines/fp8-group-gemm/baseline_dsv3_decode.py:45-53).
+
+Algorithmic bytes count every operand byte once and every output byte once;
+for the MoE workloads only the experts that received at least one pair count.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+FP8 = torch.float8_e4m3fn
+
+
+@dataclass(frozen=True)
+class Workload:
+    key: str
+    kind: str            # "linear_bf16" | "fp8_gemm" | "moe_fp8" | "moe_w4a16"
+    M: int = 0           # dense tokens
+    N: int = 0           # output rows (per expert: gate + up)
+    K: int = 0
+    T: int = 0           # MoE tokens
+    E: int = 0
+    topk: int = 0
+    routing: str = ""    # "softmax" (N(0,1) logits) | "zipf"
+    zipf_s: float = 0.0
+    bound: str = "hbm"   # roofline that limits it on MI355X
+    description: str = ""
+    seeds: dict = field(default_factory=dict)
+
+
+WORKLOADS: dict[str, Workload] = {w.key: w for w in [
+    Workload("qwen3_gateup_M16", "linear_bf16", M=16, N=24576, K=4096,
+             description="Qwen3-8B decode GateUp: X bf16 [16,4096], W bf16 [24576,4096]",
+             seeds={"x": 1, "w": 2}),
+    Workload("dsv3_fp8_M16", "fp8_gemm", M=16, N=4096, K=7168,
+             description="DeepSeek-V3 dense FP8 GEMM M=16", seeds={"a": 3, "b": 4}),
+    Workload("dsv3_fp8_M128", "fp8_gemm", M=128, N=4096, K=7168,
+             description="DeepSeek-V3 dense FP8 GEMM M=128", seeds={"a": 3, "b": 4}),
+    Workload("dsv3_fp8_M4096", "fp8_gemm", M=4096, N=4096, K=7168, bound="mfma",
+             description="DeepSeek-V3 dense FP8 GEMM M=4096", seeds={"a": 3, "b": 4}),
+    Workload("dsv3_moe_w13_decode", "moe_fp8", N=4096, K=7168, T=128, E=256, topk=8, routing="softmax",
+             description="DSv3 FP8 MoE w13 decode: 128 tokens, top-8 of 256", seeds={"logits": 5, "x": 6, "w": 100}),
+    Workload("kimi_w4a16_w13_decode", "moe_w4a16", N=4096, K=7168, T=64, E=384, topk=8, routing="softmax",
+             description="Kimi-K2 INT4 W4A16 MoE w13 decode: 64 tokens, top-8 of 384",
+             seeds={"logits": 7, "x": 8, "w": 200}),
+    Workload("dsv3_moe_w13_prefill", "moe_fp8", N=4096, K=7168, T=4096, E=256, topk=8, routing="zipf",
+             zipf_s=1.1, description="DSv3 FP8 MoE w13 prefill: 4096 tokens, Zipf(1.1) top-8 of 256",
+             seeds={"logits": 9, "x": 10, "w": 100}),
+]}
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def randn(shape, seed: int, device, std: float = 1.0) -> torch.Tensor:
+    x = torch.randn(shape, generator=_gen(seed, device), device=device, dtype=torch.float32)
+    return x * std if std != 1.0 else x
+
+
+def quant_act_1x128(x: torch.Tensor):
+    """x fp32 [M, K] -> (e4m3 [M, K], fp32 scales [M, K/128])."""
+    M, K = x.shape
+    xv = x.view(M, K // 128, 128)
+    amax = xv.abs().amax(dim=2).clamp_min(1e-4)
+    q = (xv * (448.0 / amax).unsqueeze(2)).to(FP8).view(M, K)
+    return q, amax / 448.0
+
+
+def quant_weight_128x128(w: torch.Tensor):
+    """w fp32 [N, K] -> (e4m3 [N, K], fp32 scales [N/128, K/128])."""
+    N, K = w.shape
+    wv = w.view(N // 128, 128, K // 128, 128)
+    amax = wv.abs().amax(dim=(1, 3)).clamp_min(1e-4)
+    q = (wv * (448.0 / amax)[:, None, :, None]).to(FP8).view(N, K)
+    return q, amax / 448.0
+
+
+def zipf_logits(T: int, E: int, s: float, seed: int, device) -> torch.Tensor:
+    """Gumbel-top-k logits for Zipf(s) expert popularity: -s*ln(rank) + Gumbel noise.
+
+    Top-k of these logits samples k distinct experts without replacement with
+    probability proportional to rank^-s (rank = expert id + 1).
+    """
+    u = torch.rand((T, E), generator=_gen(seed, device), device=device, dtype=torch.float32)
+    u = u.clamp(1e-12, 1.0 - 1e-7)
+    gumbel = -torch.log(-torch.log(u))
+    rank = torch.arange(1, E + 1, device=device, dtype=torch.float32)
+    return gumbel - s * torch.log(rank)[None, :]
+
+
+def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) -> dict:
+    """Generate the workload's inputs on `device`.
+
+    For MoE workloads `experts` limits which expert weights are generated (the
+    others stay zero-filled); None generates all of them.
+    """
+    s = w.seeds
+    if w.kind == "linear_bf16":
+        x = randn((w.M, w.K), s["x"], device).to(torch.bfloat16)
+        wt = randn((w.N, w.K), s["w"], device, std=0.02).to(torch.bfloat16)
+        return {"x": x, "w": wt}
+    if w.kind == "fp8_gemm":
+        a, sa = quant_act_1x128(randn((w.M, w.K), s["a"], device))
+        b, sb = quant_weight_128x128(randn((w.N, w.K), s["b"], device))
+        return {"a": a, "sa": sa, "b": b, "sb": sb}
+    if w.routing == "zipf":
+        logits = zipf_logits(w.T, w.E, w.zipf_s, s["logits"], device)
+    else:
+        logits = randn((w.T, w.E), s["logits"], device)
+    ex = range(w.E) if experts is None else experts
+    if w.kind == "moe_fp8":
+        x, sx = quant_act_1x128(randn((w.T, w.K), s["x"], device))
+        wq = torch.zeros((w.E, w.N, w.K), dtype=FP8, device=device)
+        sw = torch.ones((w.E, w.N // 128, w.K // 128), dtype=torch.float32, device=device)
+        for e in ex:
+            wq[e], sw[e] = quant_weight_128x128(randn((w.N, w.K), s["w"] + e, device))
+        return {"logits": logits, "x": x, "sx": sx, "w": wq, "sw": sw}
+    if w.kind == "moe_w4a16":
+        x = randn((w.T, w.K), s["x"], device).to(torch.bfloat16)
+        wq = torch.zeros((w.E, w.N, w.K // 8), dtype=torch.int32, device=device)
+        ws = torch.zeros((w.E, w.N, w.K // 32), dtype=torch.bfloat16, device=device)
+        for e in ex:
+            g = _gen(s["w"] + e, device)
+            wq[e] = torch.randint(-2 ** 31, 2 ** 31, (w.N, w.K // 8), generator=g, device=device, dtype=torch.int32)
+            ws[e] = (torch.randn((w.N, w.K // 32), generator=g, device=device) * 0.01).to(torch.bfloat16)
+        return {"logits": logits, "x": x, "w": wq, "ws": ws}
+    raise ValueError(w.kind)
+
+
+def experts_hit(ids: torch.Tensor, E: int) -> int:
+    return int(torch.unique(ids[(ids >= 0) & (ids < E)]).numel())
+
+
+def algorithmic_bytes(w: Workload, n_experts_hit: int = 0) -> int:
+    """Every operand byte read once + every output byte written once."""
+    if w.kind == "linear_bf16":
+        return 2 * (w.N * w.K + w.M * w.K + w.M * w.N)
+    if w.kind == "fp8_gemm":
+        return (w.M * w.K + w.M * (w.K // 128) * 4 + w.N * w.K + ((w.N + 127) // 128) * (w.K // 128) * 4
+                + w.M * w.N * 2)
+    P = w.T * w.topk
+    if w.kind == "moe_fp8":
+        per_e = w.N * w.K + (w.N // 128) * (w.K // 128) * 4
+        return (n_experts_hit * per_e + w.T * w.K + w.T * (w.K // 128) * 4 + P * (w.N // 2) * 2
+                + P * 4 * 2)  # + the pair index read twice (gather and scatter)
+    if w.kind == "moe_w4a16":
+        per_e = w.N * w.K // 2 + w.N * (w.K // 32) * 2
+        return n_experts_hit * per_e + w.T * w.K * 2 + P * (w.N // 2) * 2 + P * 4 * 2
+    raise ValueError(w.kind)
+
+
+def flops(w: Workload) -> int:
+    if w.kind in ("linear_bf16", "fp8_gemm"):
+        return 2 * w.M * w.N * w.K
+    return 2 * w.T * w.topk * w.N * w.K

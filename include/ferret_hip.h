@@ -1,0 +1,150 @@
+/*
+ * ferret_hip.h — C ABI of the MI355X (gfx950) quantized-GEMM library
+ * (libferret_hip.so).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are caller-owned DEVICE pointers; outputs are written
+ *     in place.  Nothing is allocated, nothing is freed, the host is never
+ *     synchronised: work is enqueued on `stream` (a hipStream_t; NULL = the
+ *     default stream) and returns immediately.
+ *   - Return value: 0 on success; a negative FERRET_ERR_* code for a rejected
+ *     argument (nothing was enqueued); a positive hipError_t if the launch
+ *     itself failed.  No entry point ever calls exit() or prints.
+ *   - Layouts are row-major.  bf16 tensors are passed as raw 16-bit patterns,
+ *     e4m3 tensors as bytes (OCP FP8 E4M3FN), scales as float32.
+ *   - Reentrant; thread-safe when different threads use different streams.
+ *
+ * Paths in the citations are relative to the reference repository root.
+ */
+#ifndef FERRET_HIP_H_
+#define FERRET_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FERRET_OK 0
+#define FERRET_ERR_NULL (-1)      /* a required pointer is NULL */
+#define FERRET_ERR_SHAPE (-2)     /* sizes out of range / not supported */
+#define FERRET_ERR_WORKSPACE (-3) /* workspace missing or too small */
+
+/* Library version string, e.g. "ferret-hip 0.1.0 gfx950". */
+const char* ferret_version(void);
+
+/* Human-readable text for a return code. */
+const char* ferret_error_string(int code);
+
+/*
+ * Reference ctypes ABI for the decode GEMV, kept unchanged:
+ * tests/compare_decode_linear.py:110-118 binds
+ *   launch_gemv(void* input, void* weight, void* residual, void* output,
+ *               int N, int K, void* stream)
+ * with input bf16 [1,K], weight bf16 [N,K], residual bf16 [1,N] or NULL,
+ * output bf16 [1,N].  No error return (as in the reference): on a rejected
+ * argument nothing is enqueued; ferret_linear_bf16 reports the code.
+ */
+void launch_gemv(void* input, void* weight, void* residual, void* output, int N, int K,
+                 void* stream);
+
+/*
+ * bf16 decode linear projection, y[M,N] = x[M,K] . w[N,K]^T (+ residual[M,N]),
+ * fp32 accumulation, RNE to bf16.  Replaces the host dispatch `launch_kernel`
+ * of examples/qwen3-8b-decode-linear-bs16/v019_swapab_cg2_l2hints.cu:422-482
+ * (kernel :138-391, split-K reduce :395-417).
+ * Requirements: 1 <= M, N % 16 == 0, K % 128 == 0, K/128 <= 128.
+ * `ws`/`ws_bytes` are accepted for ABI stability and may be NULL/0.
+ */
+int ferret_linear_bf16(const void* x, const void* w, const void* residual, void* y, int M, int N,
+                       int K, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Dense FP8 GEMM with DeepSeek-style fp32 block scales:
+ *   c[m,n] = sum_kb (sum_{k in kb} a[m,k] b[n,k]) * sa[m,kb] * sb[n/128,kb]
+ * a e4m3 [M,K], sa f32 [M,K/128], b e4m3 [N,K], sb f32 [ceil(N/128),K/128],
+ * c bf16 [M,N].  Replaces `run<BN,NS>` / `fp8_gemm` of
+ * examples/fp8-gemm/v002_dense_tp8_validated_065.cu:61-275 (oracle `ref` :277-288).
+ * Requirements: M >= 1, N % 16 == 0, K % 128 == 0 (N % 128 == 0 when M > 16).
+ * `ws` may be NULL (no split-K workspace is needed by the current kernels).
+ */
+int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, const float* sb,
+                               void* c, int M, int N, int K, void* ws, size_t ws_bytes,
+                               void* stream);
+
+/*
+ * Top-k routing on fp32 logits [T,E]: ids[T,topk] (int32) ordered by
+ * (logit desc, expert asc), NaN ranks as -inf; weights[T,topk] (optional,
+ * may be NULL) = softmax over all E at the chosen experts.  The reference has
+ * no routing kernel (its stand-ins: baselines/kimi-moe-w13-int4/baseline_marlin.py:92-104,
+ * baselines/fp8-group-gemm/baseline_dsv3_decode.py:50); this is the build's own
+ * contract.  Requirements: 1 <= topk <= min(E, 16), E <= 1024.
+ */
+int ferret_moe_route_topk(const float* logits, int T, int E, int topk, int32_t* ids,
+                          float* weights, void* stream);
+
+/*
+ * Expert histogram + stable permutation + tile table of routed pairs
+ * (pair p = t*topk + j).  Replaces vLLM's moe_align_block_size as called at
+ * baselines/kimi-moe-w13-int4/baseline_marlin.py:123-126 and the m_indices
+ * construction of baselines/fp8-group-gemm/baseline_dsv3_prefill.py:53.
+ * Outputs: counts[E], offsets[E+1] (exclusive cumsum), sorted_pair[P] (pairs
+ * of expert 0 in ascending order, then expert 1, ...; ids outside [0,E) are
+ * dropped), tiles[max_tiles*3] rows (expert, first sorted row, rows <= tile_m)
+ * in expert order, ntiles[1].  max_tiles must be >= ferret_moe_max_tiles().
+ * Requirements: P = T*topk <= 1<<22, E <= 1024.
+ */
+int ferret_moe_permute(const int32_t* ids, int T, int topk, int E, int tile_m, int32_t* counts,
+                       int32_t* offsets, int32_t* sorted_pair, int32_t* tiles, int max_tiles,
+                       int32_t* ntiles, void* stream);
+
+/* Upper bound on the tile count of ferret_moe_permute for P pairs. */
+int ferret_moe_max_tiles(int num_pairs, int E, int tile_m);
+
+/* Row-tile height the w13 kernels expect for a routing of P pairs over E experts
+ * (16 for decode-sized segments, 128 for prefill-sized ones). */
+int ferret_moe_tile_m(int num_pairs, int E);
+
+/*
+ * FP8 block-scaled MoE gate-up (w13) grouped GEMM with fused SiLU(gate)*up:
+ *   out[p, n] = silu(g) * u,  g = x_t . W[e][n], u = x_t . W[e][N/2 + n]
+ * for every routed pair p (token t = p / topk, expert e) using the block-scaled
+ * product of ferret_fp8_gemm_blockscale.  x e4m3 [T,K], sx f32 [T,K/128],
+ * w e4m3 [E,N,K], sw f32 [E,N/128,K/128], out bf16 [T*topk, N/2] in pair order.
+ * The tile inputs come from ferret_moe_permute with tile_m =
+ * ferret_moe_tile_m(T*topk, E).  Replaces launch_grouped_gemm_bs /
+ * grouped_fp8_gemm_bs of examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-439
+ * with the expert taken per row (not per 128-row tile, :162,286).
+ * Requirements: N % 256 == 0, K % 128 == 0.
+ */
+int ferret_moe_w13_fp8(const void* x, const float* sx, const void* w, const float* sw,
+                       const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                       int max_tiles, int tile_m, int T, int topk, int E, int N, int K, void* out,
+                       void* stream);
+
+/*
+ * INT4 W4A16 MoE gate-up (w13) grouped GEMM with fused SiLU(gate)*up.
+ * x bf16 [T,K]; wq int32 [E,N,K/8] (8 nibbles per word along K, low nibble
+ * first, value = nibble - 8); ws bf16 [E,N,K/32]; out bf16 [T*topk, N/2].
+ * Weights are dequantized in registers to bf16 = RNE(float(q) * scale) and fed
+ * to bf16 MFMA with fp32 accumulation.  Replaces ops.moe_wna16_marlin_gemm +
+ * apply_moe_activation(SILU) of baselines/kimi-moe-w13-int4/baseline_marlin.py:139-168;
+ * numerics of correctness/compare_marlin_vs_ref.py:44-100; layout of
+ * tasks/kimi-moe-w13-int4-grouped-gemm.yaml:68-83.
+ * Requirements: N % 32 == 0, K % 128 == 0, tile_m == 16.
+ */
+int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
+                         const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                         int max_tiles, int tile_m, int T, int topk, int E, int N, int K,
+                         void* out, void* stream);
+
+/* Workspace bytes an op needs (all current kernels need 0). op: 0 linear_bf16,
+ * 1 fp8_gemm_blockscale, 2 moe_w13_fp8, 3 moe_w13_w4a16. */
+size_t ferret_workspace_bytes(int op, int M, int N, int K, int E);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRET_HIP_H_ */

@@ -1,0 +1,23 @@
+"""pytest configuration: the ``gpu`` marker and shared helpers."""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The loaded HIP library (tests marked gpu only)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    from ferret_amd import lib
+    return lib.load()

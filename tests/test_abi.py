@@ -1,0 +1,65 @@
+"""CPU checks of the C-ABI boundary: the library loads and exports every declared symbol."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ferret_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)) - {"defined"})
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for must in ("launch_gemv", "ferret_linear_bf16", "ferret_fp8_gemm_blockscale", "ferret_moe_route_topk",
+                 "ferret_moe_permute", "ferret_moe_w13_fp8", "ferret_moe_w13_w4a16", "ferret_workspace_bytes"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built (run python -m ferret_amd.build)")
+    L = lib.load()
+    for name in declared_functions():
+        assert hasattr(L, name), f"{name} declared in ferret_hip.h but not exported"
+    assert set(declared_functions()) == set(lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_version_and_error_strings_without_gpu():
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    assert lib.version().startswith("ferret-hip")
+    L = lib.load()
+    assert L.ferret_error_string(-2).decode().startswith("sizes")
+    assert L.ferret_moe_max_tiles(1024, 256, 16) == 320
+    assert L.ferret_moe_tile_m(1024, 256) == 16 and L.ferret_moe_tile_m(32768, 256) == 128
+
+
+def test_argument_errors_are_returned_not_raised_without_gpu():
+    """Rejected arguments return a code before any HIP call (safe on a GPU-less host)."""
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    L = lib.load()
+    assert L.ferret_linear_bf16(None, None, None, None, 1, 16, 128, None, 0, None) == -1
+    assert L.ferret_linear_bf16(1, 1, None, 1, 1, 17, 128, None, 0, None) == -2
+    assert L.ferret_fp8_gemm_blockscale(1, 1, 1, 1, 1, 4, 64, 100, None, 0, None) == -2
+    assert L.ferret_moe_route_topk(1, 4, 2000, 8, 1, None, None) == -2
+    assert L.ferret_moe_permute(1, 4, 8, 16, 16, 1, 1, 1, 1, 0, 1, None) == -2
+    assert L.ferret_moe_w13_w4a16(1, 1, 1, 1, 1, 1, 10, 128, 4, 8, 16, 64, 256, 1, None) == -2
+
+
+def test_python_ops_refuse_cpu_tensors():
+    import torch
+    from ferret_amd import ops
+    x = torch.zeros((1, 128), dtype=torch.bfloat16)
+    w = torch.zeros((16, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.linear_bf16(x, w, out=torch.zeros((1, 16), dtype=torch.bfloat16))
