@@ -31,6 +31,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-result",
     # Packed FP32 (v_pk_*_f32) stays off: plain scalar FP32 VALU only.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ArchVGPRs: the epilogues read them with VALU ops, and the
+    # AGPR form would add a v_accvgpr_read per accumulator element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 

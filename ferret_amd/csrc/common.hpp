@@ -57,13 +57,20 @@ __device__ __forceinline__ f32x4 mfma_fp8_16x16x128(i32x8 a, i32x8 b, f32x4 c) {
 
 // 8 OCP e4m3 bytes (two dwords, byte i = element i) -> 8 bf16, exact
 // (v_cvt_scalef32_pk_bf16_fp8 with scale 1.0; every e4m3 value is a bf16 value).
-__device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-  u32x4 r;
-  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
-  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
-  return r;
+// Built with vector shuffles so the four results land in the MFMA operand
+// registers directly.
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  const bf16x4 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  const bf16x4 cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // Block-scaled FP8 partial product of one 128-wide K block on a 16x16 tile.
@@ -75,10 +82,10 @@ __device__ __forceinline__ u32x4 e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
 // tolerance of the reference check.
 __device__ __forceinline__ f32x4 fp8_block_16x16x128(u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1) {
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
-  c = mfma_bf16_16x16x32(e4m3x8_to_bf16x8(a0[0], a0[1]), e4m3x8_to_bf16x8(b0[0], b0[1]), c);
-  c = mfma_bf16_16x16x32(e4m3x8_to_bf16x8(a0[2], a0[3]), e4m3x8_to_bf16x8(b0[2], b0[3]), c);
-  c = mfma_bf16_16x16x32(e4m3x8_to_bf16x8(a1[0], a1[1]), e4m3x8_to_bf16x8(b1[0], b1[1]), c);
-  c = mfma_bf16_16x16x32(e4m3x8_to_bf16x8(a1[2], a1[3]), e4m3x8_to_bf16x8(b1[2], b1[3]), c);
+  c = mfma_bf16(e4m3x8_to_bf16x8(a0[0], a0[1]), e4m3x8_to_bf16x8(b0[0], b0[1]), c);
+  c = mfma_bf16(e4m3x8_to_bf16x8(a0[2], a0[3]), e4m3x8_to_bf16x8(b0[2], b0[3]), c);
+  c = mfma_bf16(e4m3x8_to_bf16x8(a1[0], a1[1]), e4m3x8_to_bf16x8(b1[0], b1[1]), c);
+  c = mfma_bf16(e4m3x8_to_bf16x8(a1[2], a1[3]), e4m3x8_to_bf16x8(b1[2], b1[3]), c);
   return c;
 }
 

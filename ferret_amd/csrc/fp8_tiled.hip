@@ -12,11 +12,14 @@
 // so each lane's accumulator column is one token (one activation scale per
 // token sub-tile) and the 16 weight rows of a sub-tile share one weight scale.
 //
-// Work-group: 256 threads = 4 waves (2 along weight rows x 2 along tokens),
-// tile 128 weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
-// Global -> VGPR -> LDS double buffering, one barrier per K-step; LDS rows of
-// 128 B with the 16-byte chunk index XOR-swizzled by (row & 7) so the MFMA
-// fragment reads are bank-conflict free.
+// Work-group: 512 threads = 8 waves (4 along weight rows x 2 along tokens,
+// two per SIMD so one wave's conversions overlap the other's MFMAs), tile 256
+// weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
+// Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
+// staging) through a 3-stage ring, one barrier per K-step; every load
+// instruction reads complete 128-byte lines; LDS rows of 128 B have their
+// 16-byte chunk index XOR-swizzled so the MFMA fragment reads are
+// bank-conflict free.
 //
 // Reference counterparts: fp8_gemm<BN,NS> (v002:61-249) and
 // grouped_fp8_gemm_bs<BN,NS> (examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-335),
@@ -25,11 +28,21 @@
 
 namespace ferret {
 
-constexpr int TB_N = 128;     // weight rows per work-group
-constexpr int TB_M = 128;     // tokens per work-group
-constexpr int TB_K = 128;     // K per step (one scale block)
-constexpr int TB_THREADS = 256;
-constexpr int TB_STAGE = (TB_N + TB_M) * TB_K;  // bytes per LDS stage
+constexpr int TB_WN = 4;                        // waves along the weight rows
+constexpr int TB_WM = 2;                        // waves along the tokens
+constexpr int TB_N = 64 * TB_WN;                // weight rows per work-group (256)
+constexpr int TB_M = 64 * TB_WM;                // tokens per work-group (128)
+constexpr int TB_K = 128;                       // K per step (one scale block)
+constexpr int TB_WAVES = TB_WN * TB_WM;
+constexpr int TB_THREADS = 64 * TB_WAVES;       // 512
+constexpr int TB_ROWS = TB_N + TB_M;            // 128-byte rows per stage
+constexpr int TB_LD_PER_WAVE = TB_ROWS / 8 / TB_WAVES;  // 1-KB load instructions per wave and stage
+constexpr int TB_SA_OFF = TB_ROWS * TB_K;       // token scales follow the operand rows
+constexpr int TB_STAGE = TB_SA_OFF + TB_M * 4;  // bytes per LDS stage (48.5 KB)
+constexpr int TB_NS = 3;                        // pipeline depth (stages in LDS)
+constexpr int TB_LDS = TB_NS * TB_STAGE;        // 145.5 KB of the 160 KB LDS
+static_assert(TB_ROWS % (8 * TB_WAVES) == 0, "stage rows split evenly over the waves");
+static_assert(TB_M == 128, "two token waves carry the 128 activation scales");
 
 struct TiledArgs {
   const uint8_t* a;        // e4m3 tokens [T, K]
@@ -46,22 +59,34 @@ struct TiledArgs {
   int m_blocks;            // dense: token tiles
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * TB_K + ((chunk ^ (row & 7)) << 4); }
+// Byte offset of 16-byte chunk `chunk` of stage row `row`.  Rows are 128 B;
+// the chunk index is XOR-swizzled with (row & 7) ^ ((row >> 3) & 1), which
+// keeps the 16 rows of an MFMA fragment read on distinct banks both when the
+// LDS serves 8 lanes x 16 B per cycle and when it serves 16.
+__device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * TB_K + ((chunk ^ swz_key(row)) << 4); }
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
 
 template <bool SILU>
-__global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * TB_STAGE];
+__global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wn = wave & 1;   // weight-row half of the tile
-  const int wm = wave >> 1;  // token half of the tile
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS bases in SGPRs
+  const int wn = wave % TB_WN;  // weight-row quarter of the tile
+  const int wm = wave / TB_WN;  // token half of the tile
   const int r = lane & 15;
   const int g = lane >> 4;
 
   // ---- which tile.
-  int e = 0, row0, nrows, nb, mb;
+  int e = 0, row0, nrows, nb;
   if constexpr (SILU) {
     // Grouped: bid = tile * n_blocks + nb.  Work-groups are dealt to the 8 XCDs
     // round-robin by block id and n_blocks % 8 == 0, so every tile's block nb
@@ -73,7 +98,6 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
     e = p.tiles[3 * tile_idx];
     row0 = p.tiles[3 * tile_idx + 1];
     nrows = p.tiles[3 * tile_idx + 2];
-    mb = 0;
   } else {
     // Dense: give each XCD a contiguous range of logical tiles, then raster
     // the logical tiles in groups of 8 token blocks so the work-groups resident
@@ -86,7 +110,7 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
     const int first_mb = (L / per_group) * GM;
     const int gsize = min(p.m_blocks - first_mb, GM);
     const int in_group = L % per_group;
-    mb = first_mb + in_group % gsize;
+    const int mb = first_mb + in_group % gsize;
     nb = in_group / gsize;
     row0 = mb * TB_M;
     nrows = min(TB_M, p.M - row0);
@@ -95,51 +119,93 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
   const int K = p.K, N = p.N;
   const int nkb = K / TB_K;
 
-  // ---- per-thread global source rows for the staging loads.
-  // Each thread moves 4 chunks of the weight tile and 4 of the token tile per
-  // K-step: chunk index idx = tid + 256*i -> row idx/8, 16-byte chunk idx%8.
-  const uint8_t* bsrc[4];
-  const uint8_t* asrc[4];
-  int srow[4];
+  // ---- direct-to-LDS loading.  A stage holds TB_ROWS rows of 128 B: weight
+  // rows first, then token rows, then the tile's activation scales.  Load
+  // instruction i of wave w fills stage rows (w * TB_LD_PER_WAVE + i) * 8 .. +8
+  // (1 KB; lane l -> row + l/8, LDS slot l%8, i.e. global chunk (l%8) ^ key(row)):
+  // every instruction reads 8 complete 128-B lines.  Weight rows are read with
+  // the non-temporal policy (streamed once per tile).  Addresses are a uniform
+  // base plus 32-bit per-lane offsets.
+  const uint8_t* wbase = p.b + (size_t)e * N * K;
+  uint32_t goff[TB_LD_PER_WAVE];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + TB_THREADS * i;
-    const int rr = idx >> 3;
-    const int c = idx & 7;
-    srow[i] = rr;
-    int wrow;
-    if constexpr (SILU) {
-      // rows 0..63 of the tile are gate rows nb*64.., rows 64..127 the matching up rows
-      wrow = (rr < 64) ? nb * 64 + rr : N / 2 + nb * 64 + (rr - 64);
+  for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
+    const int row = (wave * TB_LD_PER_WAVE + i) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ swz_key(row);
+    if (row < TB_N) {
+      int wrow;
+      if constexpr (SILU)
+        wrow = (row < TB_N / 2) ? nb * (TB_N / 2) + row : N / 2 + nb * (TB_N / 2) + (row - TB_N / 2);
+      else
+        wrow = min(nb * TB_N + row, N - 1);  // rows past N (last block) are loaded but never stored
+      goff[i] = (uint32_t)wrow * (uint32_t)K + chunk * 16;
     } else {
-      wrow = nb * TB_N + rr;
+      const int t = min(row - TB_N, nrows - 1);
+      const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
+      goff[i] = (uint32_t)tok * (uint32_t)K + chunk * 16;
     }
-    bsrc[i] = p.b + ((size_t)e * N + wrow) * K + c * 16;
-    const int t = min(rr, nrows - 1);
-    const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
-    asrc[i] = p.a + (size_t)tok * K + c * 16;
   }
+  // The last two waves also move the tile's 128 activation scales of the
+  // K-step into the stage (4 bytes per lane): the main loop then issues no
+  // other vector loads, so the vmcnt bookkeeping below is exact.
+  const bool sa_wave = wave >= TB_WAVES - 2;
+  const float* sa_src = nullptr;
+  if (sa_wave) {
+    const int t = min((wave - (TB_WAVES - 2)) * 64 + lane, nrows - 1);
+    const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
+    sa_src = p.sa + (size_t)tok * nkb;
+  }
+  auto issue_stage = [&](int kb) {
+    uint8_t* stage = lds + (kb % TB_NS) * TB_STAGE;
+#pragma unroll
+    for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
+      const int j = wave * TB_LD_PER_WAVE + i;  // uniform
+      uint8_t* dst = stage + j * 1024;
+      if (j * 8 < TB_N)  // cache policy 2 = nt
+        __builtin_amdgcn_global_load_lds(wbase + (size_t)kb * TB_K + goff[i], dst, 16, 0, 2);
+      else
+        __builtin_amdgcn_global_load_lds(p.a + (size_t)kb * TB_K + goff[i], dst, 16, 0, 0);
+    }
+    if (sa_wave)
+      __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
+  };
+  // This thread's copy of stage kb is complete once at most `younger` later
+  // stages remain in flight (vector-memory ops per thread and stage:
+  // TB_LD_PER_WAVE, plus one for the scale waves).
+  auto wait_stage = [&](int younger) {
+    constexpr int L = TB_LD_PER_WAVE;
+    if (!sa_wave) {
+      if (younger >= 1) wait_vmcnt<L>();
+      else wait_vmcnt<0>();
+    } else {
+      if (younger >= 1) wait_vmcnt<L + 1>();
+      else wait_vmcnt<0>();
+    }
+  };
+  static_assert(TB_NS == 3, "wait_stage counts one younger stage in flight");
 
   // ---- fragment rows of this lane
-  // weight sub-tile ni covers tile rows wn*32 + (ni&1)*16 + (ni>>1)*64 for SiLU
-  // (ni 0,1 gate; 2,3 up) and wn*64 + ni*16 for the dense case.
+  // weight sub-tile ni covers tile rows wn*32 + (ni&1)*16 + (ni>>1)*(TB_N/2) for
+  // SiLU (ni 0,1 gate; 2,3 up) and wn*64 + ni*16 for the dense case.
   int wfrag_row[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni)
-    wfrag_row[ni] = SILU ? (wn * 32 + (ni & 1) * 16 + (ni >> 1) * 64 + r) : (wn * 64 + ni * 16 + r);
+    wfrag_row[ni] = SILU ? (wn * 32 + (ni & 1) * 16 + (ni >> 1) * (TB_N / 2) + r) : (wn * 64 + ni * 16 + r);
   int afrag_row[4];
-  int tok_of[4];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    afrag_row[mi] = wm * 64 + mi * 16 + r;
-    const int t = min(afrag_row[mi], nrows - 1);
-    tok_of[mi] = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
-  }
-  // weight-scale row block (uniform per wave): dense: (nb*128 + wn*64)/128;
-  // SiLU: gate rows and up rows lie in different 128-row scale blocks.
-  const int sb_gate = SILU ? (nb * 64 + wn * 32) >> 7 : (nb * TB_N + wn * 64) >> 7;
-  const int sb_up = SILU ? (N / 2 + nb * 64 + wn * 32) >> 7 : sb_gate;
+  for (int mi = 0; mi < 4; ++mi) afrag_row[mi] = wm * 64 + mi * 16 + r;
+
+  // The wave's weight-scale rows (<= 128 K-steps) are loaded once into lanes
+  // (lane l holds K-steps l and 64 + l) before any stage is in flight; each
+  // K-step then picks its value with v_readlane, so the main loop issues no
+  // vector loads besides the stage copies.
+  const int sb_gate = SILU ? (nb * (TB_N / 2) + wn * 32) >> 7 : min(nb * TB_N + wn * 64, N - 1) >> 7;
+  const int sb_up = SILU ? (N / 2 + nb * (TB_N / 2) + wn * 32) >> 7 : sb_gate;
   const float* sbp = p.sb + (size_t)e * (N >> 7) * nkb;
+  const float sbg_lo = lane < nkb ? sbp[(size_t)sb_gate * nkb + lane] : 0.f;
+  const float sbg_hi = 64 + lane < nkb ? sbp[(size_t)sb_gate * nkb + 64 + lane] : 0.f;
+  const float sbu_lo = SILU && lane < nkb ? sbp[(size_t)sb_up * nkb + lane] : 0.f;
+  const float sbu_hi = SILU && 64 + lane < nkb ? sbp[(size_t)sb_up * nkb + 64 + lane] : 0.f;
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -147,48 +213,38 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 stg_b[4], stg_a[4];
-  auto gload = [&](int kb) {
+  // Prologue: stages 0 .. NS-2 in flight.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      stg_b[i] = ld_u32x4_stream(bsrc[i] + (size_t)kb * TB_K);
-      stg_a[i] = ld_u32x4(asrc[i] + (size_t)kb * TB_K);
-    }
-  };
-  auto lstore = [&](int buf) {
-    uint8_t* base = lds + buf * TB_STAGE;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + TB_THREADS * i;
-      const int c = idx & 7;
-      *reinterpret_cast<u32x4*>(base + swz(srow[i], c)) = stg_b[i];
-      *reinterpret_cast<u32x4*>(base + TB_N * TB_K + swz(srow[i], c)) = stg_a[i];
-    }
-  };
-
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  for (int s = 0; s < TB_NS - 1; ++s)
+    if (s < nkb) issue_stage(s);
 
   for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) gload(kb + 1);
+    // Wait for this thread's copy of stage kb; the barrier then makes every
+    // wave's part of it visible and guarantees that the ring slot refilled
+    // below (stage kb-1's) is no longer being read by any wave.
+    wait_stage(min(nkb - 1 - kb, TB_NS - 2));
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (kb + TB_NS - 1 < nkb) issue_stage(kb + TB_NS - 1);
 
-    // scales for this K-step
+    const float* sa_lds = reinterpret_cast<const float*>(lds + (kb % TB_NS) * TB_STAGE + TB_SA_OFF);
     float sa_v[4];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) sa_v[mi] = p.sa[(size_t)tok_of[mi] * nkb + kb];
-    const float sbg = sbp[(size_t)sb_gate * nkb + kb];
-    const float sbu = sbp[(size_t)sb_up * nkb + kb];
+    for (int mi = 0; mi < 4; ++mi) sa_v[mi] = sa_lds[afrag_row[mi]];
+    const float sbg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+        __builtin_bit_cast(int, kb < 64 ? sbg_lo : sbg_hi), kb & 63));
+    const float sbu = SILU ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+        __builtin_bit_cast(int, kb < 64 ? sbu_lo : sbu_hi), kb & 63)) : sbg;
 
-    const uint8_t* base = lds + buf * TB_STAGE;
+    const uint8_t* base = lds + (kb % TB_NS) * TB_STAGE;
     // Token fragments: read once per K-step and widened to bf16 (K = 32g + 8j .. +8 for MFMA j).
-    u32x4 abf[4][4];
+    bf16x8 abf[4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      const int rr = afrag_row[mi];
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(base + TB_N * TB_K + swz(rr, 2 * g));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(base + TB_N * TB_K + swz(rr, 2 * g + 1));
+      const int rr = TB_N + afrag_row[mi];
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g));
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g + 1));
       abf[mi][0] = e4m3x8_to_bf16x8(lo[0], lo[1]);
       abf[mi][1] = e4m3x8_to_bf16x8(lo[2], lo[3]);
       abf[mi][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
@@ -200,21 +256,18 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
       const int rr = wfrag_row[ni];
       const u32x4 lo = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g));
       const u32x4 hi = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g + 1));
-      const u32x4 wbf[4] = {e4m3x8_to_bf16x8(lo[0], lo[1]), e4m3x8_to_bf16x8(lo[2], lo[3]),
-                            e4m3x8_to_bf16x8(hi[0], hi[1]), e4m3x8_to_bf16x8(hi[2], hi[3])};
+      const bf16x8 wbf[4] = {e4m3x8_to_bf16x8(lo[0], lo[1]), e4m3x8_to_bf16x8(lo[2], lo[3]),
+                             e4m3x8_to_bf16x8(hi[0], hi[1]), e4m3x8_to_bf16x8(hi[2], hi[3])};
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         f32x4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) part = mfma_bf16_16x16x32(wbf[j], abf[mi][j], part);
+        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[j], abf[mi][j], part);
         const float sc = sa_v[mi] * sbv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
       }
     }
-
-    if (kb + 1 < nkb) lstore(buf ^ 1);
-    __syncthreads();
   }
 
   // ---- epilogue. acc[ni][mi][i]: weight row wfrag_row[ni] - r + 4g + i, token column r.
@@ -224,7 +277,7 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
     if (tl >= nrows) continue;
     if constexpr (SILU) {
       const int pair = p.sorted_pair[row0 + tl];
-      uint16_t* o = p.out + (size_t)pair * (N / 2) + nb * 64 + wn * 32;
+      uint16_t* o = p.out + (size_t)pair * (N / 2) + nb * (TB_N / 2) + wn * 32;
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni) {
         u32x2 v;
@@ -233,6 +286,7 @@ __global__ __launch_bounds__(TB_THREADS, 1) void fp8_tiled_kernel(TiledArgs p) {
         *reinterpret_cast<u32x2*>(o + ni * 16 + 4 * g) = v;
       }
     } else {
+      if (nb * TB_N + wn * 64 >= N) continue;  // wave's rows lie past N (N % 256 == 128)
       uint16_t* o = p.out + (size_t)(row0 + tl) * N + nb * TB_N + wn * 64;
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) {
@@ -260,10 +314,12 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
   p.M = M;
   p.N = N;
   p.K = K;
-  p.n_blocks = N / TB_N;
+  p.n_blocks = (N + TB_N - 1) / TB_N;
   p.m_blocks = (M + TB_M - 1) / TB_M;
   const int grid = p.n_blocks * p.m_blocks;
-  hipLaunchKernelGGL((fp8_tiled_kernel<false>), dim3(grid), dim3(TB_THREADS), 0, st, p);
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, TB_LDS));
+  hipLaunchKernelGGL((fp8_tiled_kernel<false>), dim3(grid), dim3(TB_THREADS), TB_LDS, st, p);
   return (int)hipGetLastError();
 }
 
@@ -282,9 +338,11 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   p.topk = topk;
   p.N = N;
   p.K = K;
-  p.n_blocks = (N / 2) / 64;
+  p.n_blocks = (N / 2) / (TB_N / 2);
   const int grid = max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
-  hipLaunchKernelGGL((fp8_tiled_kernel<true>), dim3(grid), dim3(TB_THREADS), 0, st, p);
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, TB_LDS));
+  hipLaunchKernelGGL((fp8_tiled_kernel<true>), dim3(grid), dim3(TB_THREADS), TB_LDS, st, p);
   return (int)hipGetLastError();
 }

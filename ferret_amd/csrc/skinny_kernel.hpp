@@ -1,0 +1,233 @@
+// Skinny (<= 16 token) weight-streaming GEMM kernel template for gfx950 (see
+// skinny.hip for the design notes and the entry points that instantiate it).
+#pragma once
+#include "common.hpp"
+
+namespace ferret {
+
+enum WFmt : int { kBF16 = 0, kFP8 = 1, kINT4 = 2 };
+enum EpiKind : int { kStore = 0, kSilu = 1 };
+
+struct SkinnyArgs {
+  const uint8_t* w;         // bf16 / e4m3 [G, N, K] or int32 [G, N, K/8]
+  const void* w_scale;      // FP8: f32 [G, N/128, K/128]; INT4: bf16 [G, N, K/32]
+  const uint8_t* x;         // bf16 / e4m3 [T, K]
+  const float* x_scale;     // FP8: f32 [T, K/128]
+  const uint16_t* residual; // bf16 [M, N] or null (dense store only)
+  uint16_t* out;            // dense: bf16 [M, N]; SiLU: bf16 [P, N/2]
+  const int32_t* sorted_pair;
+  const int32_t* tiles;     // grouped: int32 [max_tiles, 3]; dense: null
+  const int32_t* ntiles;
+  int topk;
+  int M;                    // dense token count
+  int N;                    // weight rows (per expert)
+  int K;
+  int units_n;              // row units per token tile
+};
+
+template <int F>
+struct FmtTraits;
+template <>
+struct FmtTraits<kBF16> {
+  static constexpr int kWVec = 4;  // u32x4 per lane per row block per K-step
+  static constexpr int kXVec = 4;
+};
+template <>
+struct FmtTraits<kFP8> {
+  static constexpr int kWVec = 2;
+  static constexpr int kXVec = 2;
+};
+template <>
+struct FmtTraits<kINT4> {
+  static constexpr int kWVec = 1;
+  static constexpr int kXVec = 4;
+};
+
+constexpr int kRedStride = 17;              // padded token stride in the LDS reduction
+constexpr int kRedBlock = 16 * kRedStride;  // floats per (wave, row block)
+
+// INT4 word (8 nibbles, low first, offset-8) -> 8 bf16 = RNE(float(q - 8) * s).
+// fma(q, s, -8s) is exact: (q - 8) * s needs <= 12 significant bits.
+__device__ __forceinline__ u32x4 dequant_int4x8(uint32_t w, float s, float ns8) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+  u32x4 d;
+  d[0] = pack_bf16x2(fmaf((float)(lo & 0xffu), s, ns8), fmaf((float)(hi & 0xffu), s, ns8));
+  d[1] = pack_bf16x2(fmaf((float)((lo >> 8) & 0xffu), s, ns8), fmaf((float)((hi >> 8) & 0xffu), s, ns8));
+  d[2] = pack_bf16x2(fmaf((float)((lo >> 16) & 0xffu), s, ns8), fmaf((float)((hi >> 16) & 0xffu), s, ns8));
+  d[3] = pack_bf16x2(fmaf((float)(lo >> 24), s, ns8), fmaf((float)(hi >> 24), s, ns8));
+  return d;
+}
+
+template <int F, int EPI, int RB, int KS, int D>
+__global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
+  constexpr int WV = FmtTraits<F>::kWVec;
+  constexpr int XV = FmtTraits<F>::kXVec;
+  constexpr int HALF = (EPI == kSilu) ? RB / 2 : RB;
+  static_assert(EPI != kSilu || RB % 2 == 0, "SiLU pairs gate and up row blocks");
+
+  extern __shared__ float red[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15;  // weight row inside a 16-row block (A side) / token column (B side)
+  const int g = lane >> 4;  // K group of the lane
+
+  const int nu = blockIdx.x % a.units_n;
+  const int tile_idx = blockIdx.x / a.units_n;
+  const bool grouped = a.tiles != nullptr;
+
+  int e = 0, row0, nrows;
+  if (grouped) {
+    if (tile_idx >= __builtin_nontemporal_load(a.ntiles)) return;  // whole work-group exits
+    e = a.tiles[3 * tile_idx];
+    row0 = a.tiles[3 * tile_idx + 1];
+    nrows = a.tiles[3 * tile_idx + 2];
+  } else {
+    row0 = tile_idx * 16;
+    nrows = min(16, a.M - row0);
+  }
+  const int tcol = min(r, nrows - 1);  // clamp: columns >= nrows compute garbage, never stored
+  const int tok = grouped ? a.sorted_pair[row0 + tcol] / a.topk : row0 + tcol;
+
+  const int N = a.N, K = a.K;
+  const int nkb = K >> 7;
+  const size_t row_bytes = (F == kBF16) ? (size_t)K * 2 : (F == kFP8 ? (size_t)K : (size_t)K / 2);
+
+  int rowb[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    if (EPI == kSilu)
+      rowb[rb] = (rb < HALF) ? (nu * HALF + rb) * 16 : N / 2 + (nu * HALF + rb - HALF) * 16;
+    else
+      rowb[rb] = (nu * RB + rb) * 16;
+  }
+  const uint8_t* wrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+    wrow[rb] = a.w + ((size_t)e * N + rowb[rb] + r) * row_bytes;
+  const uint8_t* xrow = a.x + (size_t)tok * (F == kFP8 ? (size_t)K : (size_t)K * 2);
+
+  const int ks0 = wave * KS;
+
+  u32x4 wbuf[D + 1][RB][WV];
+  u32x4 xbuf[D + 1][XV];
+  float sx[D + 1];
+  float sw[D + 1][RB];
+  uint16_t s4[D + 1][RB];
+
+  auto load = [&](int slot, int s) {
+    const int ks = ks0 + s;
+    if constexpr (F == kBF16) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wbuf[slot][rb][j] = ld_u32x4_stream(wrow[rb] + (size_t)(ks * 128 + 32 * j + 8 * g) * 2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xbuf[slot][j] = ld_u32x4(xrow + (size_t)(ks * 128 + 32 * j + 8 * g) * 2);
+    } else if constexpr (F == kFP8) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        wbuf[slot][rb][0] = ld_u32x4_stream(wrow[rb] + (size_t)ks * 128 + 32 * g);
+        wbuf[slot][rb][1] = ld_u32x4_stream(wrow[rb] + (size_t)ks * 128 + 32 * g + 16);
+        const float* swp = static_cast<const float*>(a.w_scale);
+        sw[slot][rb] = swp[((size_t)e * (N >> 7) + (rowb[rb] >> 7)) * nkb + ks];
+      }
+      xbuf[slot][0] = ld_u32x4(xrow + (size_t)ks * 128 + 32 * g);
+      xbuf[slot][1] = ld_u32x4(xrow + (size_t)ks * 128 + 32 * g + 16);
+      sx[slot] = a.x_scale[(size_t)tok * nkb + ks];
+    } else {
+      const uint16_t* sp = static_cast<const uint16_t*>(a.w_scale);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        wbuf[slot][rb][0] = ld_u32x4_stream(wrow[rb] + (size_t)ks * 64 + 16 * g);
+        s4[slot][rb] = sp[((size_t)e * N + rowb[rb] + r) * (size_t)(K >> 5) + ks * 4 + g];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xbuf[slot][j] = ld_u32x4(xrow + (size_t)(ks * 128 + 32 * g + 8 * j) * 2);
+    }
+  };
+
+  f32x4 acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < D; ++s) load(s, s);
+  // Keep the prefetches where they are written: without these barriers the
+  // scheduler sinks loads next to their first use and leaves only a few in flight.
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (s + D < KS) load((s + D) % (D + 1), s + D);
+    __builtin_amdgcn_sched_barrier(0);
+    const int slot = s % (D + 1);
+    if constexpr (F == kBF16) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rb] = mfma_bf16_16x16x32(wbuf[slot][rb][j], xbuf[slot][j], acc[rb]);
+    } else if constexpr (F == kFP8) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const f32x4 part = fp8_block_16x16x128(wbuf[slot][rb][0], wbuf[slot][rb][1], xbuf[slot][0], xbuf[slot][1]);
+        const float sc = sx[slot] * sw[slot][rb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(part[i], sc, acc[rb][i]);
+      }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float sc = bf16_bits_to_f32(s4[slot][rb]);
+        const float ns8 = -8.0f * sc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(wbuf[slot][rb][0][j], sc, ns8), xbuf[slot][j], acc[rb]);
+      }
+    }
+  }
+
+  // Cross-wave split-K reduction through LDS: red[wave][rb][token*17 + row].
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * RB + rb) * kRedBlock + r * kRedStride + 4 * g + i] = acc[rb][i];
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < 256 * HALF; idx += blockDim.x) {
+    const int part = idx >> 8;
+    const int t = (idx >> 4) & 15;
+    const int row = idx & 15;
+    if (t >= nrows) continue;
+    if constexpr (EPI == kStore) {
+      float v = 0.f;
+      for (int w = 0; w < nwaves; ++w) v += red[(w * RB + part) * kRedBlock + t * kRedStride + row];
+      const size_t o = (size_t)(row0 + t) * N + rowb[0] + part * 16 + row;
+      if (a.residual) v += bf16_bits_to_f32(a.residual[o]);
+      a.out[o] = f32_to_bf16_bits(v);
+    } else {
+      float gs = 0.f, us = 0.f;
+      for (int w = 0; w < nwaves; ++w) {
+        gs += red[(w * RB + part) * kRedBlock + t * kRedStride + row];
+        us += red[(w * RB + part + HALF) * kRedBlock + t * kRedStride + row];
+      }
+      const int pair = a.sorted_pair[row0 + t];
+      const size_t o = (size_t)pair * (N / 2) + (nu * HALF + part) * 16 + row;
+      a.out[o] = f32_to_bf16_bits(silu_mul(gs, us));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+
+template <int F, int EPI, int RB, int KS, int D>
+static int launch_one(const SkinnyArgs& a, int grid, int nwaves, hipStream_t st) {
+  const size_t lds = (size_t)nwaves * RB * kRedBlock * sizeof(float);
+  hipLaunchKernelGGL((skinny_gemm_kernel<F, EPI, RB, KS, D>), dim3(grid), dim3(nwaves * 64), lds, st, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace ferret
