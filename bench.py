@@ -369,6 +369,10 @@ def main(argv=None) -> int:
     ap.add_argument("--iters", type=int, default=300)
     ap.add_argument("--warmup-s", type=float, default=2.0)
     ap.add_argument("--flush-mb", type=int, default=512)
+    ap.add_argument("--launch-only", type=int, default=0, metavar="N",
+                    help="only launch the workload's GEMM N times (for hardware-counter runs)")
+    ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",
+                    help="only run 3 device copies of B bytes (calibrates FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the quantized-GEMM path on "
@@ -380,6 +384,22 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
+    if args.copy_bytes:
+        src = torch.empty(args.copy_bytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {args.copy_bytes} bytes x 3")
+        return 0
+    if args.launch_only:
+        from ferret_amd import workloads as W
+        r = Runner(W.WORKLOADS[args.workload], rotate_bytes=0)
+        for i in range(args.launch_only):
+            r.gemm(i)
+        torch.cuda.synchronize()
+        log(f"[bench] {args.workload}: {args.launch_only} launches")
+        return 0
     if args.kernel_result:
         return kernel_result_mode(args)
     return driver_mode(args)
