@@ -71,10 +71,13 @@ class Runner:
             wbytes = sum(t.numel() * t.element_size() for t in self.inp.values())
             ncopy = max(1, math.ceil(rotate_bytes / max(wbytes, 1)))
             self.copies += [{k: v.clone() for k, v in self.inp.items()} for _ in range(ncopy - 1)]
+        self.ws = None
         if wl.kind in ("linear_bf16", "fp8_gemm"):
             shape = (wl.M, wl.N)
             self.outs = [torch.empty(shape, dtype=torch.bfloat16, device="cuda") for _ in self.copies]
             self.n_hit = 0
+            if wl.kind == "fp8_gemm" and ops.fp8_workspace_bytes(wl.M, wl.N, wl.K):
+                self.ws = torch.empty(ops.fp8_workspace_bytes(wl.M, wl.N, wl.K), dtype=torch.uint8, device="cuda")
         else:
             self.ids, _ = ops.moe_route_topk(self.inp["logits"], wl.topk)
             self.rt = ops.moe_permute(self.ids, wl.E)
@@ -94,7 +97,7 @@ class Runner:
         if wl.kind == "linear_bf16":
             ops.linear_bf16(c["x"], c["w"], out=o)
         elif wl.kind == "fp8_gemm":
-            ops.fp8_gemm_blockscale(c["a"], c["sa"], c["b"], c["sb"], out=o)
+            ops.fp8_gemm_blockscale(c["a"], c["sa"], c["b"], c["sb"], out=o, workspace=self.ws)
         elif wl.kind == "moe_fp8":
             ops.moe_w13_fp8(c["x"], c["sx"], c["w"], c["sw"], self.rt, out=o)
         else:

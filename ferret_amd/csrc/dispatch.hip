@@ -6,7 +6,8 @@
 int ferret_fp8_gemm_skinny(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
                            int N, int K, hipStream_t st);
 int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
-                          int N, int K, hipStream_t st);
+                          int N, int K, void* ws, size_t ws_bytes, hipStream_t st);
+size_t ferret_fp8_gemm_workspace(int M, int N, int K);
 int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, const float* sw,
                               const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
                               int max_tiles, int topk, int N, int K, void* out, hipStream_t st);
@@ -28,20 +29,20 @@ extern "C" const char* ferret_error_string(int code) {
 }
 
 extern "C" size_t ferret_workspace_bytes(int op, int M, int N, int K, int E) {
-  (void)op; (void)M; (void)N; (void)K; (void)E;
+  (void)E;
+  if (op == 1 && M > 16 && M > 0 && N > 0 && K >= 128) return ferret_fp8_gemm_workspace(M, N, K);
   return 0;
 }
 
 extern "C" int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, const float* sb,
                                           void* c, int M, int N, int K, void* ws, size_t ws_bytes,
                                           void* stream) {
-  (void)ws; (void)ws_bytes;
   FERRET_REQUIRE(a && sa && b && sb && c, FERRET_ERR_NULL);
   FERRET_REQUIRE(M >= 1 && N >= 16 && K >= 128 && N % 16 == 0 && K % 128 == 0 && K / 128 <= 128,
                  FERRET_ERR_SHAPE);
   if (M <= 16) return ferret_fp8_gemm_skinny(a, sa, b, sb, c, M, N, K, (hipStream_t)stream);
   FERRET_REQUIRE(N % 128 == 0, FERRET_ERR_SHAPE);
-  return ferret_fp8_gemm_tiled(a, sa, b, sb, c, M, N, K, (hipStream_t)stream);
+  return ferret_fp8_gemm_tiled(a, sa, b, sb, c, M, N, K, ws, ws_bytes, (hipStream_t)stream);
 }
 
 extern "C" int ferret_moe_w13_fp8(const void* x, const float* sx, const void* w, const float* sw,

@@ -12,9 +12,11 @@
 // so each lane's accumulator column is one token (one activation scale per
 // token sub-tile) and the 16 weight rows of a sub-tile share one weight scale.
 //
-// Work-group: 512 threads = 8 waves (4 along weight rows x 2 along tokens,
-// two per SIMD so one wave's conversions overlap the other's MFMAs), tile 256
-// weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
+// Work-group (large M): 512 threads = 8 waves (4 along weight rows x 2 along
+// tokens, two per SIMD so one wave's conversions overlap the other's MFMAs),
+// tile 256 weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
+// Small M (<= 256) with a workspace: 64 x 128 tiles (2 waves) over K ranges
+// (split-K), fp32 partials summed in split order by a reduce kernel.
 // Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
 // staging) through a 3-stage ring, one barrier per K-step; every load
 // instruction reads complete 128-byte lines; LDS rows of 128 B have their
@@ -28,21 +30,27 @@
 
 namespace ferret {
 
-constexpr int TB_WN = 4;                        // waves along the weight rows
-constexpr int TB_WM = 2;                        // waves along the tokens
-constexpr int TB_N = 64 * TB_WN;                // weight rows per work-group (256)
-constexpr int TB_M = 64 * TB_WM;                // tokens per work-group (128)
-constexpr int TB_K = 128;                       // K per step (one scale block)
-constexpr int TB_WAVES = TB_WN * TB_WM;
-constexpr int TB_THREADS = 64 * TB_WAVES;       // 512
-constexpr int TB_ROWS = TB_N + TB_M;            // 128-byte rows per stage
-constexpr int TB_LD_PER_WAVE = TB_ROWS / 8 / TB_WAVES;  // 1-KB load instructions per wave and stage
-constexpr int TB_SA_OFF = TB_ROWS * TB_K;       // token scales follow the operand rows
-constexpr int TB_STAGE = TB_SA_OFF + TB_M * 4;  // bytes per LDS stage (48.5 KB)
-constexpr int TB_NS = 3;                        // pipeline depth (stages in LDS)
-constexpr int TB_LDS = TB_NS * TB_STAGE;        // 145.5 KB of the 160 KB LDS
-static_assert(TB_ROWS % (8 * TB_WAVES) == 0, "stage rows split evenly over the waves");
-static_assert(TB_M == 128, "two token waves carry the 128 activation scales");
+constexpr int TB_K = 128;  // K per step (one scale block)
+constexpr int TB_M = 128;  // tokens per work-group (two token waves carry the 128 activation scales)
+constexpr int TB_NS = 3;   // pipeline depth (stages in LDS)
+
+// Tile geometry: WN waves along the weight rows (64 rows each) x 2 waves along
+// the tokens (64 each).  WN = 4: 256 x 128 tile, 8 waves (two per SIMD) for
+// large M; WN = 1: 64 x 128 tile, 2 waves, used with split-K for small M.
+template <int WN>
+struct TileCfg {
+  static constexpr int kWN = WN;
+  static constexpr int kWaves = WN * 2;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kN = 64 * WN;                       // weight rows per work-group
+  static constexpr int kRows = kN + TB_M;                  // 128-byte rows per stage
+  static constexpr int kLdPerWave = kRows / 8 / kWaves;    // 1-KB load instructions per wave and stage
+  static constexpr int kSaOff = kRows * TB_K;              // token scales follow the operand rows
+  static constexpr int kStage = kSaOff + TB_M * 4;         // bytes per LDS stage
+  static constexpr int kLds = TB_NS * kStage;              // WN=4: 145.5 KB of the 160 KB LDS
+  static_assert(kRows % (8 * kWaves) == 0, "stage rows split evenly over the waves");
+  static_assert(kThreads == 128 * WN, "fp8_tiled_kernel launch bounds");
+};
 
 struct TiledArgs {
   const uint8_t* a;        // e4m3 tokens [T, K]
@@ -57,6 +65,8 @@ struct TiledArgs {
   int M, N, K;
   int n_blocks;            // work-group tiles along the weight rows (per token tile)
   int m_blocks;            // dense: token tiles
+  int k_steps;             // K-steps per split (split-K: gridDim.y splits)
+  float* partial;          // split-K: fp32 [splits, M, N] partial sums
 };
 
 // Byte offset of 16-byte chunk `chunk` of stage row `row`.  Rows are 128 B;
@@ -66,6 +76,29 @@ struct TiledArgs {
 __device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * TB_K + ((chunk ^ swz_key(row)) << 4); }
 
+// Sum the split-K fp32 partials in split order (deterministic) and round to bf16.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, size_t n4,
+                                                           uint16_t* __restrict__ out) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    f32x4 acc = reinterpret_cast<const f32x4*>(part)[i];
+    for (int s = 1; s < splits; ++s) acc += reinterpret_cast<const f32x4*>(part)[(size_t)s * n4 + i];
+    u32x2 v;
+    v[0] = pack_bf16x2(acc[0], acc[1]);
+    v[1] = pack_bf16x2(acc[2], acc[3]);
+    reinterpret_cast<u32x2*>(out)[i] = v;
+  }
+}
+
+// 16-byte-per-lane global -> LDS copies (lane l fills lds + 16 l).  Kept in
+// plain device functions: the host pass of hipcc drops a kernel template whose
+// lambdas call the 16-byte form directly.
+__device__ __forceinline__ void g2l_16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+__device__ __forceinline__ void g2l_16_nt(const void* g, void* l) {  // cache policy 2 = nt
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 2);
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -73,14 +106,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-template <bool SILU>
-__global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
+template <bool SILU, int WN, bool SPLIT>
+__global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
+  using C = TileCfg<WN>;
+  constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
+  constexpr int TB_LD_PER_WAVE = C::kLdPerWave, TB_SA_OFF = C::kSaOff, TB_STAGE = C::kStage;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS bases in SGPRs
-  const int wn = wave % TB_WN;  // weight-row quarter of the tile
+  const int wn = wave % TB_WN;  // weight-row block of the tile
   const int wm = wave / TB_WN;  // token half of the tile
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -117,7 +153,10 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
   }
 
   const int K = p.K, N = p.N;
-  const int nkb = K / TB_K;
+  const int nkb = K / TB_K;  // scale-block stride of sa / sb rows
+  // This work-group's K-steps: [kb0, kb0 + nsteps) (all of K without split-K).
+  const int kb0 = SPLIT ? blockIdx.y * p.k_steps : 0;
+  const int nsteps = SPLIT ? min(p.k_steps, nkb - kb0) : nkb;
 
   // ---- direct-to-LDS loading.  A stage holds TB_ROWS rows of 128 B: weight
   // rows first, then token rows, then the tile's activation scales.  Load
@@ -155,16 +194,17 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
     const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
     sa_src = p.sa + (size_t)tok * nkb;
   }
-  auto issue_stage = [&](int kb) {
-    uint8_t* stage = lds + (kb % TB_NS) * TB_STAGE;
+  auto issue_stage = [&](int step) {
+    uint8_t* stage = lds + (step % TB_NS) * TB_STAGE;
+    const int kb = kb0 + step;
 #pragma unroll
     for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
       const int j = wave * TB_LD_PER_WAVE + i;  // uniform
       uint8_t* dst = stage + j * 1024;
-      if (j * 8 < TB_N)  // cache policy 2 = nt
-        __builtin_amdgcn_global_load_lds(wbase + (size_t)kb * TB_K + goff[i], dst, 16, 0, 2);
+      if (j * 8 < TB_N)
+        g2l_16_nt(wbase + (size_t)kb * TB_K + goff[i], dst);
       else
-        __builtin_amdgcn_global_load_lds(p.a + (size_t)kb * TB_K + goff[i], dst, 16, 0, 0);
+        g2l_16(p.a + (size_t)kb * TB_K + goff[i], dst);
     }
     if (sa_wave)
       __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
@@ -216,19 +256,20 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
   // Prologue: stages 0 .. NS-2 in flight.
 #pragma unroll
   for (int s = 0; s < TB_NS - 1; ++s)
-    if (s < nkb) issue_stage(s);
+    if (s < nsteps) issue_stage(s);
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int step = 0; step < nsteps; ++step) {
+    const int kb = kb0 + step;
     // Wait for this thread's copy of stage kb; the barrier then makes every
     // wave's part of it visible and guarantees that the ring slot refilled
     // below (stage kb-1's) is no longer being read by any wave.
-    wait_stage(min(nkb - 1 - kb, TB_NS - 2));
+    wait_stage(min(nsteps - 1 - step, TB_NS - 2));
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (kb + TB_NS - 1 < nkb) issue_stage(kb + TB_NS - 1);
+    if (step + TB_NS - 1 < nsteps) issue_stage(step + TB_NS - 1);
 
-    const float* sa_lds = reinterpret_cast<const float*>(lds + (kb % TB_NS) * TB_STAGE + TB_SA_OFF);
+    const float* sa_lds = reinterpret_cast<const float*>(lds + (step % TB_NS) * TB_STAGE + TB_SA_OFF);
     float sa_v[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) sa_v[mi] = sa_lds[afrag_row[mi]];
@@ -237,7 +278,7 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
     const float sbu = SILU ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
         __builtin_bit_cast(int, kb < 64 ? sbu_lo : sbu_hi), kb & 63)) : sbg;
 
-    const uint8_t* base = lds + (kb % TB_NS) * TB_STAGE;
+    const uint8_t* base = lds + (step % TB_NS) * TB_STAGE;
     // Token fragments: read once per K-step and widened to bf16 (K = 32g + 8j .. +8 for MFMA j).
     bf16x8 abf[4][4];
 #pragma unroll
@@ -285,6 +326,11 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
         v[1] = pack_bf16x2(silu_mul(acc[ni][mi][2], acc[ni + 2][mi][2]), silu_mul(acc[ni][mi][3], acc[ni + 2][mi][3]));
         *reinterpret_cast<u32x2*>(o + ni * 16 + 4 * g) = v;
       }
+    } else if constexpr (SPLIT) {
+      if (nb * TB_N + wn * 64 >= N) continue;
+      float* o = p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) *reinterpret_cast<f32x4*>(o + ni * 16 + 4 * g) = acc[ni][mi];
     } else {
       if (nb * TB_N + wn * 64 >= N) continue;  // wave's rows lie past N (N % 256 == 128)
       uint16_t* o = p.out + (size_t)(row0 + tl) * N + nb * TB_N + wn * 64;
@@ -303,8 +349,34 @@ __global__ __launch_bounds__(TB_THREADS) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
+template <bool SILU, int WN, bool SPLIT>
+static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
+  using C = TileCfg<WN>;
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT>), grid, dim3(C::kThreads), C::kLds, st, p);
+  return (int)hipGetLastError();
+}
+
+// Split-K plan for small M: 64 x 128 tiles over K ranges so that the grid
+// gives every CU two work-groups (4 waves).  Returns the number of splits
+// (1 = no split-K).
+static int splitk_splits(int M, int N, int K) {
+  if (M > 256 || N % 64 != 0) return 1;
+  const int tiles = (N / 64) * ((M + TB_M - 1) / TB_M);
+  const int nkb = K / TB_K;
+  int s = 1;
+  while (tiles * s < 512 && s * 2 <= nkb / 2) s *= 2;
+  return s;
+}
+
+size_t ferret_fp8_gemm_workspace(int M, int N, int K) {
+  const int s = splitk_splits(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
 int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
-                          int N, int K, hipStream_t st) {
+                          int N, int K, void* ws, size_t ws_bytes, hipStream_t st) {
   TiledArgs p{};
   p.a = static_cast<const uint8_t*>(a);
   p.sa = sa;
@@ -314,13 +386,24 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
   p.M = M;
   p.N = N;
   p.K = K;
-  p.n_blocks = (N + TB_N - 1) / TB_N;
   p.m_blocks = (M + TB_M - 1) / TB_M;
-  const int grid = p.n_blocks * p.m_blocks;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<false>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, TB_LDS));
-  hipLaunchKernelGGL((fp8_tiled_kernel<false>), dim3(grid), dim3(TB_THREADS), TB_LDS, st, p);
-  return (int)hipGetLastError();
+  const int splits = splitk_splits(M, N, K);
+  const size_t need = ferret_fp8_gemm_workspace(M, N, K);
+  if (splits > 1 && ws != nullptr && ws_bytes >= need) {
+    const int nkb = K / TB_K;
+    p.k_steps = (nkb + splits - 1) / splits;
+    const int used = (nkb + p.k_steps - 1) / p.k_steps;  // splits actually holding K-steps
+    p.partial = static_cast<float*>(ws);
+    p.n_blocks = N / 64;
+    const int rc = launch_tiled<false, 1, true>(p, dim3(p.n_blocks * p.m_blocks, used), st);
+    if (rc != 0) return rc;
+    const size_t n4 = (size_t)M * N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
+                       static_cast<uint16_t*>(c));
+    return (int)hipGetLastError();
+  }
+  p.n_blocks = (N + TileCfg<4>::kN - 1) / TileCfg<4>::kN;
+  return launch_tiled<false, 4, false>(p, dim3(p.n_blocks * p.m_blocks), st);
 }
 
 int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, const float* sw,
@@ -338,11 +421,8 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   p.topk = topk;
   p.N = N;
   p.K = K;
-  p.n_blocks = (N / 2) / (TB_N / 2);
+  p.n_blocks = (N / 2) / (TileCfg<4>::kN / 2);
   const int grid = max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<true>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, TB_LDS));
-  hipLaunchKernelGGL((fp8_tiled_kernel<true>), dim3(grid), dim3(TB_THREADS), TB_LDS, st, p);
-  return (int)hipGetLastError();
+  return launch_tiled<true, 4, false>(p, dim3(grid), st);
 }

@@ -53,9 +53,19 @@ def linear_bf16(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor | None 
     return out
 
 
+def fp8_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Bytes of split-K workspace ferret_fp8_gemm_blockscale uses for this shape (0 if none)."""
+    return int(_lib.load().ferret_workspace_bytes(1, M, N, K, 0))
+
+
 def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
-    """c[M,N] (bf16) = block-scaled a[M,K] (e4m3) . b[N,K]^T (e4m3)."""
+                        out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """c[M,N] (bf16) = block-scaled a[M,K] (e4m3) . b[N,K]^T (e4m3).
+
+    Shapes with M <= 256 run split-K over a workspace; pass one of at least
+    fp8_workspace_bytes(M, N, K) bytes to reuse it across calls (else one is
+    taken from torch's caching allocator).
+    """
     M, K = a.shape
     N = b.shape[0]
     if b.shape[1] != K:
@@ -64,9 +74,13 @@ def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: 
         raise ValueError(f"scale shapes must be sa [M, K/128], sb [ceil(N/128), K/128]; got {tuple(sa.shape)}, {tuple(sb.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    need = fp8_workspace_bytes(M, N, K)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+    ws_ptr = _dev(workspace, "workspace") if need else None
     rc = _lib.load().ferret_fp8_gemm_blockscale(
         _dev(a, "a", (FP8, torch.uint8), 2), _dev(sa, "sa", torch.float32, 2), _dev(b, "b", (FP8, torch.uint8), 2),
-        _dev(sb, "sb", torch.float32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K, None, 0, _stream())
+        _dev(sb, "sb", torch.float32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K, ws_ptr, need, _stream())
     _lib.check("ferret_fp8_gemm_blockscale", rc)
     return out
 

@@ -67,7 +67,10 @@ int ferret_linear_bf16(const void* x, const void* w, const void* residual, void*
  * c bf16 [M,N].  Replaces `run<BN,NS>` / `fp8_gemm` of
  * examples/fp8-gemm/v002_dense_tp8_validated_065.cu:61-275 (oracle `ref` :277-288).
  * Requirements: M >= 1, N % 16 == 0, K % 128 == 0 (N % 128 == 0 when M > 16).
- * `ws` may be NULL (no split-K workspace is needed by the current kernels).
+ * For 16 < M <= 256 the product runs split-K when `ws` holds at least
+ * ferret_workspace_bytes(1, M, N, K, 0) bytes (fp32 partials, summed in a fixed
+ * order: deterministic); with ws == NULL the same result comes from the
+ * non-split kernel (slower at these shapes).
  */
 int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, const float* sb,
                                void* c, int M, int N, int K, void* ws, size_t ws_bytes,
@@ -139,8 +142,9 @@ int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
                          int max_tiles, int tile_m, int T, int topk, int E, int N, int K,
                          void* out, void* stream);
 
-/* Workspace bytes an op needs (all current kernels need 0). op: 0 linear_bf16,
- * 1 fp8_gemm_blockscale, 2 moe_w13_fp8, 3 moe_w13_w4a16. */
+/* Workspace bytes an op can use (0 = none). op: 0 linear_bf16,
+ * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
+ * 3 moe_w13_w4a16. */
 size_t ferret_workspace_bytes(int op, int M, int N, int K, int E);
 
 #ifdef __cplusplus

@@ -102,6 +102,25 @@ def test_fp8_gemm_small(ops, M, N, K):
     assert_gemm_close(bf16_out(c), ref, f"fp8 M={M}")
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 256, 1024), (77, 1024, 2048)])
+def test_fp8_gemm_split_k_and_plain_paths(hip, ops, M, N, K):
+    """16 < M <= 256: the split-K path (workspace given) and the plain path (ws NULL, or too small)."""
+    _say(f"fp8_gemm split/plain M={M} N={N} K={K}")
+    a, sa, b, sb = _fp8_inputs(M, N, K, seed=3 * M + K)
+    need = ops.fp8_workspace_bytes(M, N, K)
+    assert need >= 2 * M * N * 4, "shape expected to take the split-K path"
+    ref = G.fp8_blockscale_gemm(codes8(a), f32(sa), codes8(b), f32(sb))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    for ws_ptr, ws_bytes, tag in ((ws.data_ptr(), need, "split"), (None, 0, "null-ws"),
+                                  (ws.data_ptr(), need - 1, "short-ws")):
+        c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        rc = hip.ferret_fp8_gemm_blockscale(a.data_ptr(), sa.data_ptr(), b.data_ptr(), sb.data_ptr(), c.data_ptr(),
+                                            M, N, K, ws_ptr, ws_bytes, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert rc == 0, tag
+        assert_gemm_close(bf16_out(c), ref, f"fp8 {tag} M={M}")
+
+
 def test_fp8_gemm_power_of_two_scales_exactish(ops):
     """Small-integer e4m3 values with power-of-two scales: exact sums, only the bf16 rounding differs."""
     M, N, K = 32, 256, 512
