@@ -309,6 +309,10 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
         for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
       }
     }
+    // Ask the scheduler for its single-wave MFMA interleave (LDS reads and
+    // VALU conversions slotted between MFMAs): ~10% faster than its default
+    // order on the 4096 x 4096 x 7168 GEMM.
+    __builtin_amdgcn_iglp_opt(1);
   }
 
   // ---- epilogue. acc[ni][mi][i]: weight row wfrag_row[ni] - r + 4g + i, token column r.
