@@ -246,8 +246,23 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
 
 # ---------------------------------------------------------------------------- modes
 
+def settle_clocks(runner, seconds: float = 0.5) -> None:
+    """Run the step untimed for `seconds` so the GPU leaves its idle clocks
+    before the warmup steps (a few ms of warmup alone measures the ramp)."""
+    import torch
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        runner.step(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_steps(runner, steps: int, warmup: int):
     import torch
+    settle_clocks(runner)
     for i in range(warmup):
         runner.step(i)
     torch.cuda.synchronize()

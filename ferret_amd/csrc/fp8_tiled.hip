@@ -18,10 +18,14 @@
 // Small M (<= 256) with a workspace: 64 x 128 tiles (2 waves) over K ranges
 // (split-K), fp32 partials summed in split order by a reduce kernel.
 // Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
-// staging) through a 3-stage ring, one barrier per K-step; every load
-// instruction reads complete 128-byte lines; LDS rows of 128 B have their
-// 16-byte chunk index XOR-swizzled so the MFMA fragment reads are
-// bank-conflict free.
+// staging) through a 3-stage ring; every load instruction reads complete
+// 128-byte lines; LDS rows of 128 B have their 16-byte chunk index
+// XOR-swizzled so the MFMA fragment reads are bank-conflict free.
+// Per K-step a wave widens its fragments (128 v_cvt_scalef32_pk_bf16_fp8) and
+// issues 64 MFMAs and 64 scale folds.  With full token tiles the two waves of
+// a SIMD run these halves out of phase (ping-pong, two barriers per K-step);
+// a partial tile (grouped GEMM) instead runs one barrier per K-step and skips
+// the MFMAs and widening of its empty 16-token sub-tiles.
 //
 // Reference counterparts: fp8_gemm<BN,NS> (v002:61-249) and
 // grouped_fp8_gemm_bs<BN,NS> (examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-335),
@@ -32,7 +36,6 @@ namespace ferret {
 
 constexpr int TB_K = 128;  // K per step (one scale block)
 constexpr int TB_M = 128;  // tokens per work-group (two token waves carry the 128 activation scales)
-constexpr int TB_NS = 3;   // pipeline depth (stages in LDS)
 
 // Tile geometry: WN waves along the weight rows (64 rows each) x 2 waves along
 // the tokens (64 each).  WN = 4: 256 x 128 tile, 8 waves (two per SIMD) for
@@ -43,13 +46,22 @@ struct TileCfg {
   static constexpr int kWaves = WN * 2;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kN = 64 * WN;                       // weight rows per work-group
-  static constexpr int kRows = kN + TB_M;                  // 128-byte rows per stage
-  static constexpr int kLdPerWave = kRows / 8 / kWaves;    // 1-KB load instructions per wave and stage
-  static constexpr int kSaOff = kRows * TB_K;              // token scales follow the operand rows
+  static constexpr int kWBytes = kN * TB_K;                // weight rows (e4m3) of a stage
+  static constexpr int kABytes = TB_M * TB_K;              // token rows (e4m3) of a stage
+  static constexpr int kWInstr = kWBytes / 1024;           // 1-KB load instructions for the weights
+  static constexpr int kLdPerWave = (kWBytes + kABytes) / 1024 / kWaves;
+  static constexpr int kSaOff = kWBytes + kABytes;         // token scales follow the operand rows
   static constexpr int kStage = kSaOff + TB_M * 4;         // bytes per LDS stage
-  static constexpr int kLds = TB_NS * kStage;              // WN=4: 145.5 KB of the 160 KB LDS
-  static_assert(kRows % (8 * kWaves) == 0, "stage rows split evenly over the waves");
+  static constexpr int kNS = 3;                            // stages in the ring
+  static constexpr int kLds = kNS * kStage;                // WN=4: 145.5 KB of the 160 KB LDS
+  static_assert((kWBytes + kABytes) % (1024 * kWaves) == 0, "stage loads split evenly over the waves");
+  static_assert(kLds <= 160 * 1024, "LDS budget");
   static_assert(kThreads == 128 * WN, "fp8_tiled_kernel launch bounds");
+};
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
 };
 
 struct TiledArgs {
@@ -106,11 +118,12 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-template <bool SILU, int WN, bool SPLIT>
+template <bool SILU, int WN, bool SPLIT, bool PP>
 __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   using C = TileCfg<WN>;
   constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
   constexpr int TB_LD_PER_WAVE = C::kLdPerWave, TB_SA_OFF = C::kSaOff, TB_STAGE = C::kStage;
+  constexpr int TB_NS = C::kNS;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
   const int tid = threadIdx.x;
@@ -158,20 +171,22 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   const int kb0 = SPLIT ? blockIdx.y * p.k_steps : 0;
   const int nsteps = SPLIT ? min(p.k_steps, nkb - kb0) : nkb;
 
-  // ---- direct-to-LDS loading.  A stage holds TB_ROWS rows of 128 B: weight
-  // rows first, then token rows, then the tile's activation scales.  Load
-  // instruction i of wave w fills stage rows (w * TB_LD_PER_WAVE + i) * 8 .. +8
-  // (1 KB; lane l -> row + l/8, LDS slot l%8, i.e. global chunk (l%8) ^ key(row)):
-  // every instruction reads 8 complete 128-B lines.  Weight rows are read with
+  // ---- direct-to-LDS loading.  A stage holds the weight rows, then the token
+  // rows (128 B of e4m3 each), then the tile's activation scales.  Load
+  // instruction j (= w * TB_LD_PER_WAVE + i for wave w) fills stage bytes
+  // j KB .. +1 KB: lane l -> row j*8 + l/8 of its part, LDS slot l%8 holding
+  // global chunk (l%8) ^ key(row), so every instruction reads eight complete
+  // 128-B lines.  Weight rows are read with
   // the non-temporal policy (streamed once per tile).  Addresses are a uniform
   // base plus 32-bit per-lane offsets.
   const uint8_t* wbase = p.b + (size_t)e * N * K;
   uint32_t goff[TB_LD_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
-    const int row = (wave * TB_LD_PER_WAVE + i) * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ swz_key(row);
-    if (row < TB_N) {
+    const int j = wave * TB_LD_PER_WAVE + i;
+    if (j < C::kWInstr) {
+      const int row = j * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ swz_key(row);
       int wrow;
       if constexpr (SILU)
         wrow = (row < TB_N / 2) ? nb * (TB_N / 2) + row : N / 2 + nb * (TB_N / 2) + (row - TB_N / 2);
@@ -179,7 +194,9 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
         wrow = min(nb * TB_N + row, N - 1);  // rows past N (last block) are loaded but never stored
       goff[i] = (uint32_t)wrow * (uint32_t)K + chunk * 16;
     } else {
-      const int t = min(row - TB_N, nrows - 1);
+      const int row = (j - C::kWInstr) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ swz_key(row);
+      const int t = min(row, nrows - 1);
       const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
       goff[i] = (uint32_t)tok * (uint32_t)K + chunk * 16;
     }
@@ -201,7 +218,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
       const int j = wave * TB_LD_PER_WAVE + i;  // uniform
       uint8_t* dst = stage + j * 1024;
-      if (j * 8 < TB_N)
+      if (j < C::kWInstr)
         g2l_16_nt(wbase + (size_t)kb * TB_K + goff[i], dst);
       else
         g2l_16(p.a + (size_t)kb * TB_K + goff[i], dst);
@@ -258,34 +275,32 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   for (int s = 0; s < TB_NS - 1; ++s)
     if (s < nsteps) issue_stage(s);
 
-  for (int step = 0; step < nsteps; ++step) {
+  // One K-step is two phases: X (LDS fragment reads + e4m3 -> bf16 widening,
+  // VALU only) and Y (the MFMAs + the scale folds).  Fragments widened by X
+  // live in registers until Y.  Both take the number MI of 16-token sub-tiles
+  // of this wave that hold tokens (a partial tile of a grouped GEMM skips the
+  // empty ones; MI is uniform per wave).
+  bf16x8 abf[4][4], wbf[4][4];
+  float sa_v[4], sbg = 0.f, sbu = 0.f;
+  auto phase_x = [&](auto mic, int step) {
+    constexpr int MI = decltype(mic)::value;
     const int kb = kb0 + step;
-    // Wait for this thread's copy of stage kb; the barrier then makes every
-    // wave's part of it visible and guarantees that the ring slot refilled
-    // below (stage kb-1's) is no longer being read by any wave.
-    wait_stage(min(nsteps - 1 - step, TB_NS - 2));
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if (step + TB_NS - 1 < nsteps) issue_stage(step + TB_NS - 1);
-
-    const float* sa_lds = reinterpret_cast<const float*>(lds + (step % TB_NS) * TB_STAGE + TB_SA_OFF);
-    float sa_v[4];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) sa_v[mi] = sa_lds[afrag_row[mi]];
-    const float sbg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-        __builtin_bit_cast(int, kb < 64 ? sbg_lo : sbg_hi), kb & 63));
-    const float sbu = SILU ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-        __builtin_bit_cast(int, kb < 64 ? sbu_lo : sbu_hi), kb & 63)) : sbg;
-
     const uint8_t* base = lds + (step % TB_NS) * TB_STAGE;
-    // Token fragments: read once per K-step and widened to bf16 (K = 32g + 8j .. +8 for MFMA j).
-    bf16x8 abf[4][4];
+    const float* sa_lds = reinterpret_cast<const float*>(base + TB_SA_OFF);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int rr = TB_N + afrag_row[mi];
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g + 1));
+    for (int mi = 0; mi < MI; ++mi) sa_v[mi] = sa_lds[afrag_row[mi]];
+    sbg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+        __builtin_bit_cast(int, kb < 64 ? sbg_lo : sbg_hi), kb & 63));
+    sbu = SILU ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+        __builtin_bit_cast(int, kb < 64 ? sbu_lo : sbu_hi), kb & 63)) : sbg;
+    // K = 32g + 8j .. +8 feeds MFMA j of every sub-tile.
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const int t = afrag_row[mi];
+      const uint8_t* arow = base + C::kWBytes + t * TB_K;
+      const int key = swz_key(t);
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(arow + (((2 * g) ^ key) << 4));
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(arow + (((2 * g + 1) ^ key) << 4));
       abf[mi][0] = e4m3x8_to_bf16x8(lo[0], lo[1]);
       abf[mi][1] = e4m3x8_to_bf16x8(lo[2], lo[3]);
       abf[mi][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
@@ -293,26 +308,93 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     }
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
-      const float sbv = (SILU && ni >= 2) ? sbu : sbg;
       const int rr = wfrag_row[ni];
       const u32x4 lo = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g));
       const u32x4 hi = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g + 1));
-      const bf16x8 wbf[4] = {e4m3x8_to_bf16x8(lo[0], lo[1]), e4m3x8_to_bf16x8(lo[2], lo[3]),
-                             e4m3x8_to_bf16x8(hi[0], hi[1]), e4m3x8_to_bf16x8(hi[2], hi[3])};
+      wbf[ni][0] = e4m3x8_to_bf16x8(lo[0], lo[1]);
+      wbf[ni][1] = e4m3x8_to_bf16x8(lo[2], lo[3]);
+      wbf[ni][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
+      wbf[ni][3] = e4m3x8_to_bf16x8(hi[2], hi[3]);
+    }
+  };
+  auto phase_y = [&](auto mic) {
+    constexpr int MI = decltype(mic)::value;
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
+    for (int ni = 0; ni < 4; ++ni) {
+      const float sbv = (SILU && ni >= 2) ? sbu : sbg;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
         f32x4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[j], abf[mi][j], part);
+        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[ni][j], abf[mi][j], part);
         const float sc = sa_v[mi] * sbv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
       }
     }
-    // Ask the scheduler for its single-wave MFMA interleave (LDS reads and
-    // VALU conversions slotted between MFMAs): ~10% faster than its default
-    // order on the 4096 x 4096 x 7168 GEMM.
+  };
+  // One K-step of the single-phase loop.  The interleave hint asks the
+  // scheduler for its single-wave MFMA order (LDS reads and VALU widening
+  // slotted between MFMAs): ~7% faster than its default order on the
+  // 4096 x 4096 x 7168 GEMM.
+  auto step_xy = [&](auto mic, int step) {
+    phase_x(mic, step);
+    phase_y(mic);
     __builtin_amdgcn_iglp_opt(1);
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Barrier that opens K-step `step`: this thread's copy of the stage is
+  // complete before it, every wave's after it; the ring slot refilled right
+  // after it (stage step-1's) has been read by every wave by then.
+  auto open_step = [&](int step) {
+    if (step < nsteps) wait_stage(min(nsteps - 1 - step, TB_NS - 2));
+    barrier();
+    if (step + TB_NS - 1 < nsteps) issue_stage(step + TB_NS - 1);
+  };
+
+  if constexpr (PP) {
+    // Ping-pong (full token tiles): waves w and w + WN share a SIMD (work-group
+    // waves are dealt to the four SIMDs round-robin), so the token-half-0 waves
+    // run X while their SIMD partners run Y of the previous K-step, and vice
+    // versa; the MFMAs of one wave overlap the VALU widening of the other.  Both
+    // halves pass the same 2 * nsteps + 1 barriers.
+    if (wm == 0) {
+      for (int step = 0; step < nsteps; ++step) {
+        open_step(step);
+        phase_x(IntC<4>{}, step);
+        barrier();
+        phase_y(IntC<4>{});
+      }
+      open_step(nsteps);
+    } else {
+      open_step(0);
+      for (int step = 0; step < nsteps; ++step) {
+        barrier();
+        phase_x(IntC<4>{}, step);
+        open_step(step + 1);
+        phase_y(IntC<4>{});
+      }
+    }
+  } else {
+    // 16-token sub-tiles of this wave holding tokens (uniform per wave); one
+    // K-loop per count, so that each is scheduled for its own MI.
+    auto k_loop = [&](auto mic) {
+      for (int step = 0; step < nsteps; ++step) {
+        open_step(step);
+        if constexpr (decltype(mic)::value > 0) step_xy(mic, step);
+      }
+    };
+    switch (max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
+      case 4: k_loop(IntC<4>{}); break;
+      case 3: k_loop(IntC<3>{}); break;
+      case 2: k_loop(IntC<2>{}); break;
+      case 1: k_loop(IntC<1>{}); break;
+      default: k_loop(IntC<0>{}); break;
+    }
   }
 
   // ---- epilogue. acc[ni][mi][i]: weight row wfrag_row[ni] - r + 4g + i, token column r.
@@ -353,12 +435,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
-template <bool SILU, int WN, bool SPLIT>
+template <bool SILU, int WN, bool SPLIT, bool PP>
 static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
   using C = TileCfg<WN>;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT>,
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT, PP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
-  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT>), grid, dim3(C::kThreads), C::kLds, st, p);
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT, PP>), grid, dim3(C::kThreads), C::kLds, st, p);
   return (int)hipGetLastError();
 }
 
@@ -399,15 +481,18 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     const int used = (nkb + p.k_steps - 1) / p.k_steps;  // splits actually holding K-steps
     p.partial = static_cast<float*>(ws);
     p.n_blocks = N / 64;
-    const int rc = launch_tiled<false, 1, true>(p, dim3(p.n_blocks * p.m_blocks, used), st);
+    const int rc = launch_tiled<false, 1, true, false>(p, dim3(p.n_blocks * p.m_blocks, used), st);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
                        static_cast<uint16_t*>(c));
     return (int)hipGetLastError();
   }
-  p.n_blocks = (N + TileCfg<4>::kN - 1) / TileCfg<4>::kN;
-  return launch_tiled<false, 4, false>(p, dim3(p.n_blocks * p.m_blocks), st);
+  // Dense tiles: ping-pong when every token tile is full (M % 128 == 0),
+  // else the single-phase loop, which skips a partial tile's empty sub-tiles.
+  p.n_blocks = (N + 255) / 256;
+  if (M % TB_M == 0) return launch_tiled<false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st);
+  return launch_tiled<false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st);
 }
 
 int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, const float* sw,
@@ -425,8 +510,8 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   p.topk = topk;
   p.N = N;
   p.K = K;
-  p.n_blocks = (N / 2) / (TileCfg<4>::kN / 2);
+  p.n_blocks = (N / 2) / 128;
   const int grid = max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
-  return launch_tiled<true, 4, false>(p, dim3(grid), st);
+  return launch_tiled<true, 4, false, false>(p, dim3(grid), st);
 }
