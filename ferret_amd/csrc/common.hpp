@@ -108,6 +108,27 @@ __device__ __forceinline__ u32x4 ld_u32x4_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Global -> LDS copies (global_load_lds): lane l fills lds + size * l; the LDS
+// base is taken from the wave's first lane.  Kept in plain device functions:
+// the host pass of hipcc drops a kernel template whose lambdas call the
+// 16-byte form directly.
+__device__ __forceinline__ void g2l_16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+__device__ __forceinline__ void g2l_16_nt(const void* g, void* l) {  // cache policy 2 = nt
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 2);
+}
+__device__ __forceinline__ void g2l_4(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }

@@ -101,23 +101,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-// 16-byte-per-lane global -> LDS copies (lane l fills lds + 16 l).  Kept in
-// plain device functions: the host pass of hipcc drops a kernel template whose
-// lambdas call the 16-byte form directly.
-__device__ __forceinline__ void g2l_16(const void* g, void* l) {
-  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
-}
-__device__ __forceinline__ void g2l_16_nt(const void* g, void* l) {  // cache policy 2 = nt
-  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 2);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
 template <bool SILU, int WN, bool SPLIT, bool PP>
 __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   using C = TileCfg<WN>;

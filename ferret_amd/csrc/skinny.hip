@@ -18,8 +18,42 @@
 // grouped_fp8_gemm_bs (examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-335);
 // the INT4 w13 contract (tasks/kimi-moe-w13-int4-grouped-gemm.yaml:68-95,150-167).
 #include "skinny_kernel.hpp"
+#include "stream_kernel.hpp"
 
 namespace ferret {
+
+// Compute units of the current device (the persistent grid size).
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Stream-kernel launch (persistent grid, one work-group of 8 waves per CU):
+// returns 1 if the shape is not covered (the caller then uses the per-unit
+// kernel), else the launch status.  KS = K-steps per wave = K / 128 / 8.
+template <int F, int EPI, int RB, int D>
+static int try_stream(const SkinnyArgs& a, int dense_tiles, int max_tiles, hipStream_t st) {
+  constexpr int NW = 8;
+  const int nkb = a.K >> 7;
+  if (nkb % NW != 0) return 1;
+  const int grid = cu_count();
+  // A work-group's tile table must fit its LDS copy.
+  const int tiles = a.tiles ? max_tiles : dense_tiles;
+  const long per = ((long)tiles * a.units_n + grid - 1) / grid;
+  if (a.tiles && per / a.units_n + 2 > kStreamMaxTiles) return 1;
+  switch (nkb / NW) {
+    case 4: return launch_stream<F, EPI, RB, NW, 4, D>(a, dense_tiles, grid, st);
+    case 7: return launch_stream<F, EPI, RB, NW, 7, D>(a, dense_tiles, grid, st);
+  }
+  return 1;
+}
 
 // K-steps per wave: prefer a split giving 4..16 waves (balanced reduction
 // against per-wave stream depth), else any split with <= 16 waves.
@@ -76,6 +110,10 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   a.N = N;
   a.K = K;
   a.units_n = N / 16;
+  if (residual == nullptr) {
+    const int rc = try_stream<kBF16, kStore, 1, 3>(a, (M + 15) / 16, 0, (hipStream_t)stream);
+    if (rc != 1) return rc;
+  }
   return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, (hipStream_t)stream);
 }
 
@@ -98,6 +136,8 @@ int ferret_fp8_gemm_skinny(const void* a_, const float* sa, const void* b, const
   a.N = N;
   a.K = K;
   a.units_n = N / 16;
+  const int rc = try_stream<kFP8, kStore, 1, 6>(a, (M + 15) / 16, 0, st);
+  if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, (M + 15) / 16, st);
 }
 
@@ -118,6 +158,9 @@ int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, con
   a.N = N;
   a.K = K;
   a.units_n = N / 32;
+  if (max_tiles <= 0) return FERRET_OK;
+  const int rc = try_stream<kFP8, kSilu, 2, 3>(a, 0, max_tiles, st);
+  if (rc != 1) return rc;
   return launch_skinny<kFP8, kSilu, 2>(a, max_tiles, st);
 }
 
@@ -140,5 +183,8 @@ extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void
   a.N = N;
   a.K = K;
   a.units_n = N / 32;
+  if (max_tiles <= 0) return FERRET_OK;
+  const int rc = try_stream<kINT4, kSilu, 2, 5>(a, 0, max_tiles, (hipStream_t)stream);
+  if (rc != 1) return rc;
   return launch_skinny<kINT4, kSilu, 2>(a, max_tiles, (hipStream_t)stream);
 }

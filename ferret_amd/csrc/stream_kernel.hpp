@@ -1,0 +1,329 @@
+// Persistent weight-streaming GEMM for decode-sized token tiles (<= 16 tokens)
+// on gfx950: the HBM-bound bf16 / FP8 / INT4 linear projections and MoE w13
+// grouped GEMMs.
+//
+// Work decomposition.  A unit is (token tile, RB blocks of 16 weight rows); a
+// work-group of NW waves owns a contiguous range of units (a persistent grid
+// of ~2 work-groups per CU), and within a unit wave w takes the K-steps
+// [w*KS, (w+1)*KS) (one K-step = 128 K = one fp32 scale block), so the unit's
+// partial sums meet once, in LDS, at the end of the unit.
+//
+// Data movement.  Weights go global -> LDS with global_load_lds_dwordx4
+// (no VGPR staging) into a ring of D stages private to each wave; every DMA
+// instruction reads complete 128-byte lines (8 lanes per line).  A wave waits
+// only for its own copies (vmcnt), so the main loop has no barrier, and the
+// ring runs ahead across unit boundaries.  LDS rows keep their 16-byte chunks
+// XOR-swizzled so the MFMA fragment reads are free of bank conflicts.  The
+// tile's activations (and FP8 activation scales) are loaded once per token
+// tile into registers: a wave holds its K-range of x for the whole range of
+// units that share the tile.
+//
+// Math (swap-AB): weight rows are the MFMA A side, tokens the B side; lane
+// (r, g) of a 16x16x32 bf16 MFMA j carries K = 32g + 8j .. +8 of the K-step
+// for both operands.  FP8 weights are widened to bf16 (exact) and each K-step
+// is folded into the fp32 accumulator with sa * sb; INT4 words are dequantized
+// to bf16 = RNE((q - 8) * s) (the group-32 scale sits in the stage next to the
+// weights).
+#pragma once
+#include "skinny_kernel.hpp"
+
+namespace ferret {
+
+template <int F>
+struct StreamFmt;
+template <>
+struct StreamFmt<kBF16> {
+  static constexpr int kRowB = 256;  // bytes of one weight row per K-step
+  static constexpr int kInstr = 4;   // 1-KB DMA instructions per 16-row block and K-step
+};
+template <>
+struct StreamFmt<kFP8> {
+  static constexpr int kRowB = 128;
+  static constexpr int kInstr = 2;
+};
+template <>
+struct StreamFmt<kINT4> {
+  static constexpr int kRowB = 64;
+  static constexpr int kInstr = 1;
+};
+
+constexpr int kStreamMaxTiles = 64;  // token tiles one work-group may touch (tile table in LDS)
+
+template <int F, int RB, int NW, int D>
+struct StreamCfg {
+  static constexpr int kWBytes = RB * 16 * StreamFmt<F>::kRowB;       // weights of one stage
+  // + 256 B of per-stage scales: the FP8 weight-block scale of each row block,
+  // or the INT4 group scales of the 32 rows (4 groups x bf16 each).
+  static constexpr int kStage = kWBytes + (F == kBF16 ? 0 : 256);
+  static constexpr int kLoads = RB * StreamFmt<F>::kInstr + (F == kBF16 ? 0 : 1);  // DMA ops per stage
+  static constexpr int kRing = D * kStage;                            // per wave
+  static constexpr int kRed = NW * RB * kRedBlock * 4;                // one reduction buffer
+  static constexpr int kTiles = kStreamMaxTiles * 3 * 4;              // grouped tile table
+  static constexpr int kLds = NW * kRing + 2 * kRed + kTiles;
+  static_assert(F != kINT4 || RB == 2, "INT4 scale copy covers two row blocks");
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert(D >= 1 && D * kLoads < 64, "vmcnt range");
+};
+
+// Chunk slot of global 16-byte chunk c of LDS row `row` (per row width).
+__device__ __forceinline__ int sw_bf16(int row, int c) { return c ^ (((row & 7) << 1) | ((row >> 3) & 1)); }
+__device__ __forceinline__ int sw_fp8(int row, int c) { return c ^ ((row & 7) ^ ((row >> 3) & 1)); }
+__device__ __forceinline__ int sw_int4(int row, int c) { return c ^ ((row >> 2) & 3); }
+
+// s_waitcnt vmcnt(min(n, N) * L) for a wave-uniform n >= 0.
+template <int L, int N>
+__device__ __forceinline__ void wait_items(int n) {
+  if constexpr (N == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= N) {
+      wait_vmcnt<N * L>();
+      return;
+    }
+    wait_items<L, N - 1>(n);
+  }
+}
+
+// s_waitcnt lgkmcnt(0) only (LDS writes done before a barrier).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+template <int F, int EPI, int RB, int NW, int KS, int D>
+__global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int dense_tiles) {
+  using C = StreamCfg<F, RB, NW, D>;
+  constexpr int ROWB = StreamFmt<F>::kRowB;
+  constexpr int NI = StreamFmt<F>::kInstr;
+  constexpr int L = C::kLoads;
+  static_assert(EPI != kSilu || RB == 2, "SiLU units pair one gate and one up block");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const bool grouped = a.tiles != nullptr;
+  const int N = a.N, K = a.K;
+  const int nkb = K >> 7;
+  const size_t wrow_bytes = (size_t)K * ROWB / 128;
+
+  // ---- this work-group's units
+  const int ntiles = grouped ? __builtin_amdgcn_readfirstlane(a.ntiles[0]) : dense_tiles;
+  const int units = ntiles * a.units_n;
+  const int per = (units + gridDim.x - 1) / gridDim.x;
+  const int u_begin = min(units, (int)blockIdx.x * per);
+  const int u_end = min(units, u_begin + per);
+  const int n_items = (u_end - u_begin) * KS;
+  if (n_items == 0) return;
+
+  uint8_t* ring = lds + wave * C::kRing;
+  float* red = reinterpret_cast<float*>(lds + NW * C::kRing);
+  int* tinfo = reinterpret_cast<int*>(lds + NW * C::kRing + 2 * C::kRed);
+
+  // Grouped: copy this work-group's rows of the tile table to LDS once, so the
+  // loop reads them without vector-memory loads (which would drain the ring).
+  const int t_first = u_begin / a.units_n;
+  if (grouped) {
+    const int t_last = (u_end - 1) / a.units_n;
+    for (int i = threadIdx.x; i < 3 * (t_last - t_first + 1); i += NW * 64) tinfo[i] = a.tiles[3 * t_first + i];
+    __syncthreads();
+  }
+
+  // Row block rb of unit-in-tile nu: first weight row.
+  auto block_row = [&](int nu, int rb) {
+    if constexpr (EPI == kSilu) return rb == 0 ? nu * 16 : N / 2 + nu * 16;
+    else return (nu * RB + rb) * 16;
+  };
+  auto tile_expert = [&](int tile) { return grouped ? tinfo[3 * (tile - t_first)] : 0; };
+
+  // ---- DMA issue cursor (uniform): unit iu, K-step is of this wave.
+  // Lane offsets inside a 16-row block are the same for every unit.
+  uint32_t lane_off[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    int row, slot;
+    if constexpr (F == kBF16) { row = 4 * i + (lane >> 4); slot = lane & 15; }
+    else if constexpr (F == kFP8) { row = 8 * i + (lane >> 3); slot = lane & 7; }
+    else { row = lane >> 2; slot = lane & 3; }
+    int c;
+    if constexpr (F == kBF16) c = sw_bf16(row, slot);
+    else if constexpr (F == kFP8) c = sw_fp8(row, slot);
+    else c = sw_int4(row, slot);
+    lane_off[i] = (uint32_t)row * (uint32_t)wrow_bytes + c * 16;
+  }
+  int iu = u_begin, is = 0;
+  const uint8_t* ibase[RB];
+  const uint8_t* isc = nullptr;  // this lane's per-stage scale source for the unit
+  auto set_issue_unit = [&](int u) {
+    const int tile = u / a.units_n, nu = u % a.units_n;
+    const int e = tile_expert(tile);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      ibase[rb] = a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)wave * KS * ROWB;
+    if constexpr (F == kINT4) {
+      // lane l: dword l & 1 (groups 2(l&1), +1) of row (l & 31) / 2 of block l / 32
+      const int rb = lane >> 5, row = (lane & 31) >> 1;
+      isc = static_cast<const uint8_t*>(a.w_scale) +
+            (((size_t)e * N + block_row(nu, rb) + row) * (size_t)(K >> 5) + (size_t)wave * KS * 4) * 2 + (lane & 1) * 4;
+    } else if constexpr (F == kFP8) {
+      // lane l < RB: the 128 x 128 weight-scale of block l (other lanes repeat the last)
+      const int rb = min(lane, RB - 1);
+      isc = static_cast<const uint8_t*>(a.w_scale) +
+            (((size_t)e * (N >> 7) + (block_row(nu, rb) >> 7)) * (size_t)nkb + (size_t)wave * KS) * 4;
+    }
+  };
+  auto issue = [&](int slot) {
+    uint8_t* st = ring + slot * C::kStage;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        g2l_16_nt(ibase[rb] + (size_t)is * ROWB + lane_off[i], st + (rb * NI + i) * 1024);
+    if constexpr (F == kINT4) g2l_4(isc + is * 8, st + C::kWBytes);
+    if constexpr (F == kFP8) g2l_4(isc + is * 4, st + C::kWBytes);
+    if (++is == KS) {
+      is = 0;
+      if (++iu < u_end) set_issue_unit(iu);
+    }
+  };
+
+  set_issue_unit(iu);
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < n_items) issue(d);
+
+  // ---- activations of the current token tile (registers), per K-step of this wave
+  constexpr int XV = (F == kFP8) ? 2 : 4;
+  u32x4 xv[KS][XV];
+  float sx[KS];
+  int cur_tile = -1;
+  int my_pair = 0;  // SiLU: routed pair of token column r (from sorted_pair)
+  int nrows = 0, row0 = 0;
+
+  f32x4 acc[RB];
+  int buf = 0;
+
+  for (int u = u_begin; u < u_end; ++u) {
+    const int tile = u / a.units_n;
+    const int nu = u % a.units_n;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (tile != cur_tile) {
+      cur_tile = tile;
+      if (grouped) {
+        row0 = tinfo[3 * (tile - t_first) + 1];
+        nrows = tinfo[3 * (tile - t_first) + 2];
+      } else {
+        row0 = tile * 16;
+        nrows = min(16, a.M - row0);
+      }
+      const int tcol = min(r, nrows - 1);  // columns >= nrows compute garbage, never stored
+      int tok = row0 + tcol;
+      if (grouped) {
+        my_pair = a.sorted_pair[row0 + tcol];
+        tok = my_pair / a.topk;
+      }
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int ks = wave * KS + k;
+        if constexpr (F == kFP8) {
+          const uint8_t* xp = a.x + (size_t)tok * K + (size_t)ks * 128 + 32 * g;
+          xv[k][0] = ld_u32x4(xp);
+          xv[k][1] = ld_u32x4(xp + 16);
+          sx[k] = a.x_scale[(size_t)tok * nkb + ks];
+        } else {
+          const uint8_t* xp = a.x + ((size_t)tok * K + (size_t)ks * 128 + 32 * g) * 2;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
+        }
+      }
+      wait_vmcnt<0>();  // once per token tile: drains the ring as well
+    }
+
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int it = (u - u_begin) * KS + s;
+      // Wait for this item's stage (items issued after it may stay in flight).
+      wait_items<L, D - 1>(min(D - 1, n_items - 1 - it));
+      __builtin_amdgcn_sched_barrier(0);
+      const int slot = it % D;
+      const uint8_t* st = ring + slot * C::kStage;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const uint8_t* blk = st + rb * 16 * ROWB + r * ROWB;
+        if constexpr (F == kBF16) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const u32x4 wf = *reinterpret_cast<const u32x4*>(blk + (sw_bf16(r, 4 * g + j) << 4));
+            acc[rb] = mfma_bf16_16x16x32(wf, xv[s][j], acc[rb]);
+          }
+        } else if constexpr (F == kFP8) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g) << 4));
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g + 1) << 4));
+          const f32x4 part = fp8_block_16x16x128(lo, hi, xv[s][0], xv[s][1]);
+          const float sb = *reinterpret_cast<const float*>(st + C::kWBytes + 4 * rb);
+          const float sc = sx[s] * sb;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(part[i], sc, acc[rb][i]);
+        } else {
+          const u32x4 wq = *reinterpret_cast<const u32x4*>(blk + (sw_int4(r, g) << 4));
+          const uint16_t sbits =
+              *reinterpret_cast<const uint16_t*>(st + C::kWBytes + (rb * 16 + r) * 8 + g * 2);
+          const float sc = bf16_bits_to_f32(sbits);
+          const float ns8 = -8.0f * sc;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(wq[j], sc, ns8), xv[s][j], acc[rb]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // Refill the slot just read (its fragments are in registers by now).
+      if (it + D < n_items) issue(slot);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- unit end: cross-wave K reduction through LDS, then the epilogue.
+    float* rb_base = red + buf * (C::kRed / 4);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rb_base[(wave * RB + rb) * kRedBlock + r * kRedStride + 4 * g + i] = acc[rb][i];
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EPI == kStore) {
+      for (int idx = threadIdx.x; idx < RB * 256; idx += NW * 64) {
+        const int part = idx >> 8, t = (idx >> 4) & 15, row = idx & 15;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += rb_base[(w * RB + part) * kRedBlock + t * kRedStride + row];
+        if (t < nrows) a.out[(size_t)(row0 + t) * N + block_row(nu, part) + row] = f32_to_bf16_bits(v);
+      }
+    } else {
+      const int idx = threadIdx.x;
+      const int t = (idx >> 4) & 15, row = idx & 15;
+      // pair of token column t: held by lane t of every wave
+      const int pair = __shfl(my_pair, t, 64);
+      if (idx < 256 && t < nrows) {
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          gs += rb_base[(w * RB + 0) * kRedBlock + t * kRedStride + row];
+          us += rb_base[(w * RB + 1) * kRedBlock + t * kRedStride + row];
+        }
+        a.out[(size_t)pair * (N / 2) + nu * 16 + row] = f32_to_bf16_bits(silu_mul(gs, us));
+      }
+    }
+    buf ^= 1;
+  }
+}
+
+template <int F, int EPI, int RB, int NW, int KS, int D>
+static int launch_stream(const SkinnyArgs& a, int dense_tiles, int grid, hipStream_t st) {
+  using C = StreamCfg<F, RB, NW, D>;
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)stream_gemm_kernel<F, EPI, RB, NW, KS, D>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
+  hipLaunchKernelGGL((stream_gemm_kernel<F, EPI, RB, NW, KS, D>), dim3(grid), dim3(NW * 64), C::kLds, st, a,
+                     dense_tiles);
+  return (int)hipGetLastError();
+}
+
+}  // namespace ferret

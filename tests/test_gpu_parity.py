@@ -43,7 +43,8 @@ def test_single_hip_runtime(hip):
 # ------------------------------------------------------------------ bf16 linear
 
 @pytest.mark.parametrize("M,N,K,res", [(1, 64, 128, False), (5, 256, 512, True), (16, 512, 4096, False),
-                                       (16, 128, 12288, True), (20, 96, 1024, False), (3, 48, 896, True)])
+                                       (16, 128, 12288, True), (20, 96, 1024, False), (3, 48, 896, True),
+                                       (20, 256, 4096, False), (9, 1024, 7168, False), (33, 48, 4096, False)])
 def test_linear_bf16_small(ops, M, N, K, res):
     _say(f"linear_bf16 M={M} N={N} K={K} res={res}")
     g = torch.Generator(device="cuda").manual_seed(M * 1000 + N + K)
@@ -195,7 +196,8 @@ def _moe_fp8_small(T, E, N, K, topk, seed):
 
 @pytest.mark.parametrize("T,E,N,K,topk,tile_m", [(16, 8, 256, 256, 2, 16), (40, 6, 512, 1024, 3, 16),
                                                  (300, 4, 256, 512, 2, 128), (64, 16, 512, 896, 4, 128),
-                                                 (3, 5, 256, 128, 5, 16)])
+                                                 (3, 5, 256, 128, 5, 16), (24, 6, 512, 4096, 3, 16),
+                                                 (40, 12, 256, 7168, 8, 16)])
 def test_moe_w13_fp8_small(ops, T, E, N, K, topk, tile_m):
     _say(f"moe_w13_fp8 T={T} E={E} N={N} K={K} topk={topk} tile_m={tile_m}")
     x, sx, w, sw, logits = _moe_fp8_small(T, E, N, K, topk, seed=T + E + N)
@@ -208,7 +210,7 @@ def test_moe_w13_fp8_small(ops, T, E, N, K, topk, tile_m):
 
 
 @pytest.mark.parametrize("T,E,N,K,topk", [(8, 8, 64, 256, 2), (64, 12, 256, 1024, 8), (5, 3, 32, 128, 3),
-                                          (32, 16, 128, 7168, 4)])
+                                          (32, 16, 128, 7168, 4), (24, 6, 512, 4096, 3)])
 def test_moe_w13_w4a16_small(ops, T, E, N, K, topk):
     _say(f"moe_w13_w4a16 T={T} E={E} N={N} K={K} topk={topk}")
     g = torch.Generator(device="cuda").manual_seed(T + E + N + K)
