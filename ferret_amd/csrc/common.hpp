@@ -21,6 +21,12 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// Compile-time integer as a value (for generic lambdas over tile shapes).
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
 // ---------------------------------------------------------------- conversions
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {

@@ -59,11 +59,6 @@ struct TileCfg {
   static_assert(kThreads == 128 * WN, "fp8_tiled_kernel launch bounds");
 };
 
-template <int V>
-struct IntC {
-  static constexpr int value = V;
-};
-
 struct TiledArgs {
   const uint8_t* a;        // e4m3 tokens [T, K]
   const float* sa;         // [T, K/128]

@@ -35,22 +35,26 @@ static int cu_count() {
   return cached[dev];
 }
 
-// Stream-kernel launch (persistent grid, one work-group of 8 waves per CU):
+// Stream-kernel launch (persistent grid, one work-group of NW waves per CU):
 // returns 1 if the shape is not covered (the caller then uses the per-unit
-// kernel), else the launch status.  KS = K-steps per wave = K / 128 / 8.
-template <int F, int EPI, int RB, int D>
+// kernel), else the launch status.  KS = K-steps per wave = K / 128 / NW.
+template <int F, int EPI, int RB, int D, int NW = 8>
 static int try_stream(const SkinnyArgs& a, int dense_tiles, int max_tiles, hipStream_t st) {
-  constexpr int NW = 8;
   const int nkb = a.K >> 7;
   if (nkb % NW != 0) return 1;
+  // INT4 unit scales are copied as 16-byte chunks of the scale rows.
+  if (F == kINT4 && ((reinterpret_cast<uintptr_t>(a.w_scale) & 15) != 0 || a.K % 256 != 0)) return 1;
   const int grid = cu_count();
   // A work-group's tile table must fit its LDS copy.
   const int tiles = a.tiles ? max_tiles : dense_tiles;
   const long per = ((long)tiles * a.units_n + grid - 1) / grid;
   if (a.tiles && per / a.units_n + 2 > kStreamMaxTiles) return 1;
+  // INT4 keeps at most one unit of scales ahead: ring depth <= KS.
+  constexpr int D4 = (F == kINT4 && D > 4) ? 4 : D;
   switch (nkb / NW) {
-    case 4: return launch_stream<F, EPI, RB, NW, 4, D>(a, dense_tiles, grid, st);
+    case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, dense_tiles, grid, st);
     case 7: return launch_stream<F, EPI, RB, NW, 7, D>(a, dense_tiles, grid, st);
+    case 8: return launch_stream<F, EPI, RB, NW, 8, D>(a, dense_tiles, grid, st);
   }
   return 1;
 }
@@ -111,7 +115,10 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   a.K = K;
   a.units_n = N / 16;
   if (residual == nullptr) {
-    const int rc = try_stream<kBF16, kStore, 1, 3>(a, (M + 15) / 16, 0, (hipStream_t)stream);
+#ifndef STREAM_BF16_CFG
+#define STREAM_BF16_CFG 1, 3, 8
+#endif
+    const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, (hipStream_t)stream);
     if (rc != 1) return rc;
   }
   return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, (hipStream_t)stream);
@@ -136,7 +143,10 @@ int ferret_fp8_gemm_skinny(const void* a_, const float* sa, const void* b, const
   a.N = N;
   a.K = K;
   a.units_n = N / 16;
-  const int rc = try_stream<kFP8, kStore, 1, 6>(a, (M + 15) / 16, 0, st);
+#ifndef STREAM_FP8_CFG
+#define STREAM_FP8_CFG 1, 6, 8
+#endif
+  const int rc = try_stream<kFP8, kStore, STREAM_FP8_CFG>(a, (M + 15) / 16, 0, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, (M + 15) / 16, st);
 }
@@ -159,7 +169,10 @@ int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, con
   a.K = K;
   a.units_n = N / 32;
   if (max_tiles <= 0) return FERRET_OK;
-  const int rc = try_stream<kFP8, kSilu, 2, 3>(a, 0, max_tiles, st);
+#ifndef STREAM_MOE_CFG
+#define STREAM_MOE_CFG 2, 3, 8
+#endif
+  const int rc = try_stream<kFP8, kSilu, STREAM_MOE_CFG>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kSilu, 2>(a, max_tiles, st);
 }
@@ -184,7 +197,10 @@ extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void
   a.K = K;
   a.units_n = N / 32;
   if (max_tiles <= 0) return FERRET_OK;
-  const int rc = try_stream<kINT4, kSilu, 2, 5>(a, 0, max_tiles, (hipStream_t)stream);
+#ifndef STREAM_INT4_CFG
+#define STREAM_INT4_CFG 2, 5, 8
+#endif
+  const int rc = try_stream<kINT4, kSilu, STREAM_INT4_CFG>(a, 0, max_tiles, (hipStream_t)stream);
   if (rc != 1) return rc;
   return launch_skinny<kINT4, kSilu, 2>(a, max_tiles, (hipStream_t)stream);
 }

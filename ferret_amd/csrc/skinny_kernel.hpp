@@ -46,11 +46,20 @@ struct FmtTraits<kINT4> {
 constexpr int kRedStride = 17;              // padded token stride in the LDS reduction
 constexpr int kRedBlock = 16 * kRedStride;  // floats per (wave, row block)
 
+// x & 0x0F0F0F0F through inline asm: hiding the known-zero bits from the
+// compiler keeps it converting bytes with v_cvt_f32_ubyte{0..3} (one op each)
+// instead of extracting every nibble with v_bfe_u32 first.
+__device__ __forceinline__ uint32_t nibbles_as_bytes(uint32_t x) {
+  uint32_t r;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // INT4 word (8 nibbles, low first, offset-8) -> 8 bf16 = RNE(float(q - 8) * s).
 // fma(q, s, -8s) is exact: (q - 8) * s needs <= 12 significant bits.
 __device__ __forceinline__ u32x4 dequant_int4x8(uint32_t w, float s, float ns8) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+  const uint32_t lo = nibbles_as_bytes(w);
+  const uint32_t hi = nibbles_as_bytes(w >> 4);
   u32x4 d;
   d[0] = pack_bf16x2(fmaf((float)(lo & 0xffu), s, ns8), fmaf((float)(hi & 0xffu), s, ns8));
   d[1] = pack_bf16x2(fmaf((float)((lo >> 8) & 0xffu), s, ns8), fmaf((float)((hi >> 8) & 0xffu), s, ns8));

@@ -49,20 +49,27 @@ struct StreamFmt<kINT4> {
 
 constexpr int kStreamMaxTiles = 64;  // token tiles one work-group may touch (tile table in LDS)
 
-template <int F, int RB, int NW, int D>
+template <int F, int RB, int NW, int KS, int D>
 struct StreamCfg {
   static constexpr int kWBytes = RB * 16 * StreamFmt<F>::kRowB;       // weights of one stage
-  // + 256 B of per-stage scales: the FP8 weight-block scale of each row block,
-  // or the INT4 group scales of the 32 rows (4 groups x bf16 each).
-  static constexpr int kStage = kWBytes + (F == kBF16 ? 0 : 256);
-  static constexpr int kLoads = RB * StreamFmt<F>::kInstr + (F == kBF16 ? 0 : 1);  // DMA ops per stage
+  // FP8: + 256 B per stage for the 128 x 128 weight-block scale of each row block.
+  static constexpr int kStage = kWBytes + (F == kFP8 ? 256 : 0);
+  static constexpr int kLoads = RB * StreamFmt<F>::kInstr + (F == kFP8 ? 1 : 0);  // DMA ops per stage
   static constexpr int kRing = D * kStage;                            // per wave
+  // INT4: the group scales of a unit (RB * 16 rows x this wave's KS K-steps,
+  // 8 B per row and K-step) are copied once per unit as whole 16-B chunks:
+  // kSclCh chunks per row cover the wave's (8-B aligned) span, double-buffered
+  // by unit parity; kSclLoads DMA ops (16 B per lane) per unit.
+  static constexpr int kSclCh = (KS * 8 + 8 + 15) / 16;
+  static constexpr int kSclBuf = RB * 16 * kSclCh * 16;
+  static constexpr int kSclLoads = F == kINT4 ? (RB * 16 * kSclCh + 63) / 64 : 0;
+  static constexpr int kScl = F == kINT4 ? 2 * kSclBuf : 0;            // per wave
   static constexpr int kRed = NW * RB * kRedBlock * 4;                // one reduction buffer
   static constexpr int kTiles = kStreamMaxTiles * 3 * 4;              // grouped tile table
-  static constexpr int kLds = NW * kRing + 2 * kRed + kTiles;
-  static_assert(F != kINT4 || RB == 2, "INT4 scale copy covers two row blocks");
+  static constexpr int kLds = NW * (kRing + kScl) + 2 * kRed + kTiles;
+  static_assert(F != kINT4 || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(D >= 1 && D * kLoads < 64, "vmcnt range");
+  static_assert(D >= 1 && D * kLoads + kSclLoads < 64, "vmcnt range");
 };
 
 // Chunk slot of global 16-byte chunk c of LDS row `row` (per row width).
@@ -70,17 +77,29 @@ __device__ __forceinline__ int sw_bf16(int row, int c) { return c ^ (((row & 7) 
 __device__ __forceinline__ int sw_fp8(int row, int c) { return c ^ ((row & 7) ^ ((row >> 3) & 1)); }
 __device__ __forceinline__ int sw_int4(int row, int c) { return c ^ ((row >> 2) & 3); }
 
-// s_waitcnt vmcnt(min(n, N) * L) for a wave-uniform n >= 0.
-template <int L, int N>
+// Wait until item S of a unit (K-step S of KS) has landed, while the
+// min(n, N) items issued after it may stay in flight: each item is L DMA ops,
+// and the first item of a unit also carries SI ops (the unit's INT4 scales),
+// so one of those later items adds SI when the next unit starts within them.
+template <int L, int SI, int KS, int S, int N>
 __device__ __forceinline__ void wait_items(int n) {
   if constexpr (N == 0) {
     wait_vmcnt<0>();
   } else {
     if (n >= N) {
-      wait_vmcnt<N * L>();
+      wait_vmcnt<N * L + ((KS - S) <= N ? SI : 0)>();
       return;
     }
-    wait_items<L, N - 1>(n);
+    wait_items<L, SI, KS, S, N - 1>(n);
+  }
+}
+
+// f(IntC<0>{}), ..., f(IntC<N-1>{}) in order.
+template <int I, int N, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    static_for<I + 1, N>(f);
   }
 }
 
@@ -89,7 +108,7 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 
 template <int F, int EPI, int RB, int NW, int KS, int D>
 __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int dense_tiles) {
-  using C = StreamCfg<F, RB, NW, D>;
+  using C = StreamCfg<F, RB, NW, KS, D>;
   constexpr int ROWB = StreamFmt<F>::kRowB;
   constexpr int NI = StreamFmt<F>::kInstr;
   constexpr int L = C::kLoads;
@@ -114,9 +133,10 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   const int n_items = (u_end - u_begin) * KS;
   if (n_items == 0) return;
 
-  uint8_t* ring = lds + wave * C::kRing;
-  float* red = reinterpret_cast<float*>(lds + NW * C::kRing);
-  int* tinfo = reinterpret_cast<int*>(lds + NW * C::kRing + 2 * C::kRed);
+  uint8_t* ring = lds + wave * (C::kRing + C::kScl);
+  uint8_t* sclbuf = ring + C::kRing;  // INT4 unit scales (two buffers)
+  float* red = reinterpret_cast<float*>(lds + NW * (C::kRing + C::kScl));
+  int* tinfo = reinterpret_cast<int*>(lds + NW * (C::kRing + C::kScl) + 2 * C::kRed);
 
   // Grouped: copy this work-group's rows of the tile table to LDS once, so the
   // loop reads them without vector-memory loads (which would drain the ring).
@@ -151,7 +171,15 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   }
   int iu = u_begin, is = 0;
   const uint8_t* ibase[RB];
-  const uint8_t* isc = nullptr;  // this lane's per-stage scale source for the unit
+  const uint8_t* isc = nullptr;  // FP8: this lane's per-stage scale source for the unit
+  // INT4: this wave's span of a scale row is [s_start, s_start + KS*8) bytes;
+  // copy op q, lane l covers chunk (q*64 + l) % kSclCh of unit row (q*64 + l) / kSclCh.
+  constexpr int SCH = C::kSclCh, SI = C::kSclLoads;
+  const int s_start = wave * KS * 8;
+  const int s_a0 = s_start & ~15;
+  const int s_nch = (s_start + KS * 8 - s_a0 + 15) / 16;
+  const uint8_t* sc_src[SI > 0 ? SI : 1];
+  bool sc_live[SI > 0 ? SI : 1];
   auto set_issue_unit = [&](int u) {
     const int tile = u / a.units_n, nu = u % a.units_n;
     const int e = tile_expert(tile);
@@ -159,10 +187,14 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     for (int rb = 0; rb < RB; ++rb)
       ibase[rb] = a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)wave * KS * ROWB;
     if constexpr (F == kINT4) {
-      // lane l: dword l & 1 (groups 2(l&1), +1) of row (l & 31) / 2 of block l / 32
-      const int rb = lane >> 5, row = (lane & 31) >> 1;
-      isc = static_cast<const uint8_t*>(a.w_scale) +
-            (((size_t)e * N + block_row(nu, rb) + row) * (size_t)(K >> 5) + (size_t)wave * KS * 4) * 2 + (lane & 1) * 4;
+#pragma unroll
+      for (int q = 0; q < SI; ++q) {
+        const int idx = q * 64 + lane, row = idx / SCH, ch = idx % SCH;
+        sc_live[q] = row < RB * 16 && ch < s_nch;
+        const int rr = min(row, RB * 16 - 1);
+        sc_src[q] = static_cast<const uint8_t*>(a.w_scale) +
+                    ((size_t)e * N + block_row(nu, rr >> 4) + (rr & 15)) * (size_t)(K >> 4) + s_a0 + ch * 16;
+      }
     } else if constexpr (F == kFP8) {
       // lane l < RB: the 128 x 128 weight-scale of block l (other lanes repeat the last)
       const int rb = min(lane, RB - 1);
@@ -177,8 +209,15 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 #pragma unroll
       for (int i = 0; i < NI; ++i)
         g2l_16_nt(ibase[rb] + (size_t)is * ROWB + lane_off[i], st + (rb * NI + i) * 1024);
-    if constexpr (F == kINT4) g2l_4(isc + is * 8, st + C::kWBytes);
     if constexpr (F == kFP8) g2l_4(isc + is * 4, st + C::kWBytes);
+    if constexpr (F == kINT4) {
+      if (is == 0) {
+        uint8_t* sb = sclbuf + (iu & 1) * C::kSclBuf;
+#pragma unroll
+        for (int q = 0; q < SI; ++q)
+          if (sc_live[q]) g2l_16(sc_src[q], sb + q * 1024);
+      }
+    }
     if (++is == KS) {
       is = 0;
       if (++iu < u_end) set_issue_unit(iu);
@@ -238,11 +277,12 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       wait_vmcnt<0>();  // once per token tile: drains the ring as well
     }
 
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
+    const uint8_t* sb_unit = sclbuf + (u & 1) * C::kSclBuf;
+    static_for<0, KS>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
       const int it = (u - u_begin) * KS + s;
       // Wait for this item's stage (items issued after it may stay in flight).
-      wait_items<L, D - 1>(min(D - 1, n_items - 1 - it));
+      wait_items<L, SI, KS, s, D - 1>(min(D - 1, n_items - 1 - it));
       __builtin_amdgcn_sched_barrier(0);
       const int slot = it % D;
       const uint8_t* st = ring + slot * C::kStage;
@@ -265,8 +305,8 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
           for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(part[i], sc, acc[rb][i]);
         } else {
           const u32x4 wq = *reinterpret_cast<const u32x4*>(blk + (sw_int4(r, g) << 4));
-          const uint16_t sbits =
-              *reinterpret_cast<const uint16_t*>(st + C::kWBytes + (rb * 16 + r) * 8 + g * 2);
+          const uint16_t sbits = *reinterpret_cast<const uint16_t*>(
+              sb_unit + (rb * 16 + r) * (SCH * 16) + (s_start - s_a0) + s * 8 + g * 2);
           const float sc = bf16_bits_to_f32(sbits);
           const float ns8 = -8.0f * sc;
 #pragma unroll
@@ -278,7 +318,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       // Refill the slot just read (its fragments are in registers by now).
       if (it + D < n_items) issue(slot);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
 
     // ---- unit end: cross-wave K reduction through LDS, then the epilogue.
     float* rb_base = red + buf * (C::kRed / 4);
@@ -318,7 +358,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 
 template <int F, int EPI, int RB, int NW, int KS, int D>
 static int launch_stream(const SkinnyArgs& a, int dense_tiles, int grid, hipStream_t st) {
-  using C = StreamCfg<F, RB, NW, D>;
+  using C = StreamCfg<F, RB, NW, KS, D>;
   FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)stream_gemm_kernel<F, EPI, RB, NW, KS, D>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
   hipLaunchKernelGGL((stream_gemm_kernel<F, EPI, RB, NW, KS, D>), dim3(grid), dim3(NW * 64), C::kLds, st, a,
