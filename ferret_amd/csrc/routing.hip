@@ -162,18 +162,21 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
   }
   __syncthreads();
 
-  // Stable placement, chunk by chunk in pair order.
+  // Stable placement, chunk by chunk in pair order (the next chunk's ids are
+  // loaded while this one is placed).
+  int e_next = (tid < P) ? ids[tid] : -1;
   for (int base = 0; base < P; base += kPermThreads) {
     const int p = base + tid;
-    int e = (p < P) ? ids[p] : -1;
+    int e = e_next;
+    e_next = (p + kPermThreads < P) ? ids[p + kPermThreads] : -1;
     const bool valid = e >= 0 && e < E;
     if (!valid) e = -1;
     // rank among earlier lanes of this wave with the same expert
     int rank = 0;
     uint64_t remaining = __ballot(valid);
     while (remaining) {
-      const int leader = __ffsll((unsigned long long)remaining) - 1;
-      const int le = __shfl(e, leader);
+      const int leader = __ffsll((unsigned long long)remaining) - 1;  // wave-uniform
+      const int le = __builtin_amdgcn_readlane(e, leader);
       const uint64_t m = __ballot(valid && e == le);
       if (valid && e == le) {
         const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));

@@ -9,8 +9,8 @@
 // partial sums meet once, in LDS, at the end of the unit.
 //
 // Data movement.  Weights go global -> LDS with global_load_lds_dwordx4
-// (no VGPR staging) into a ring of D stages private to each wave; every DMA
-// instruction reads complete 128-byte lines (8 lanes per line).  A wave waits
+// (no VGPR staging) into a ring of D stages private to each wave; every bf16 /
+// FP8 DMA instruction reads complete 128-byte lines (8 lanes per line).  A wave waits
 // only for its own copies (vmcnt), so the main loop has no barrier, and the
 // ring runs ahead across unit boundaries.  LDS rows keep their 16-byte chunks
 // XOR-swizzled so the MFMA fragment reads are free of bank conflicts.  The
@@ -204,11 +204,17 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   };
   auto issue = [&](int slot) {
     uint8_t* st = ring + slot * C::kStage;
+    // Weight rows are streamed once: non-temporal, except INT4, whose 64-byte
+    // row slice per K-step is half a line -- the other half is the wave's next
+    // K-step and must still be in L2 when it is read.
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
-        g2l_16_nt(ibase[rb] + (size_t)is * ROWB + lane_off[i], st + (rb * NI + i) * 1024);
+      for (int i = 0; i < NI; ++i) {
+        const uint8_t* src = ibase[rb] + (size_t)is * ROWB + lane_off[i];
+        if constexpr (F == kINT4) g2l_16(src, st + (rb * NI + i) * 1024);
+        else g2l_16_nt(src, st + (rb * NI + i) * 1024);
+      }
     if constexpr (F == kFP8) g2l_4(isc + is * 4, st + C::kWBytes);
     if constexpr (F == kINT4) {
       if (is == 0) {

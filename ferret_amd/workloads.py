@@ -53,7 +53,7 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
              description="Kimi-K2 INT4 W4A16 MoE w13 decode: 64 tokens, top-8 of 384",
              seeds={"logits": 7, "x": 8, "w": 200}),
     Workload("dsv3_moe_w13_prefill", "moe_fp8", N=4096, K=7168, T=4096, E=256, topk=8, routing="zipf",
-             zipf_s=1.1, description="DSv3 FP8 MoE w13 prefill: 4096 tokens, Zipf(1.1) top-8 of 256",
+             zipf_s=1.1, bound="mfma", description="DSv3 FP8 MoE w13 prefill: 4096 tokens, Zipf(1.1) top-8 of 256",
              seeds={"logits": 9, "x": 10, "w": 100}),
 ]}
 
