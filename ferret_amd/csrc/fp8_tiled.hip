@@ -422,15 +422,25 @@ static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-// Split-K plan for small M: 64 x 128 tiles over K ranges so that the grid
-// gives every CU two work-groups (4 waves).  Returns the number of splits
-// (1 = no split-K).
+// Split-K plan for small M: 128 x 128 tiles (4 waves) over K ranges, the
+// number of splits doubled until the grid covers the 256 CUs once (measured
+// on 128 x 4096 x 7168 against 64 x 128 and 256 x 128 tiles and 2 grids per
+// CU: 28 us vs 29-36 us).  Returns the number of splits (1 = no split-K).
+#ifndef SPLITK_WN
+#define SPLITK_WN 2
+#endif
+#ifndef SPLITK_TARGET
+#define SPLITK_TARGET 256
+#endif
+#ifndef SPLITK_PP
+#define SPLITK_PP false
+#endif
 static int splitk_splits(int M, int N, int K) {
-  if (M > 256 || N % 64 != 0) return 1;
-  const int tiles = (N / 64) * ((M + TB_M - 1) / TB_M);
+  if (M > 256 || N % (64 * SPLITK_WN) != 0) return 1;
+  const int tiles = (N / (64 * SPLITK_WN)) * ((M + TB_M - 1) / TB_M);
   const int nkb = K / TB_K;
   int s = 1;
-  while (tiles * s < 512 && s * 2 <= nkb / 2) s *= 2;
+  while (tiles * s < SPLITK_TARGET && s * 2 <= nkb / 2) s *= 2;
   return s;
 }
 
@@ -458,8 +468,8 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     p.k_steps = (nkb + splits - 1) / splits;
     const int used = (nkb + p.k_steps - 1) / p.k_steps;  // splits actually holding K-steps
     p.partial = static_cast<float*>(ws);
-    p.n_blocks = N / 64;
-    const int rc = launch_tiled<false, 1, true, false>(p, dim3(p.n_blocks * p.m_blocks, used), st);
+    p.n_blocks = N / (64 * SPLITK_WN);
+    const int rc = launch_tiled<false, SPLITK_WN, true, SPLITK_PP>(p, dim3(p.n_blocks * p.m_blocks, used), st);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,

@@ -110,30 +110,13 @@ __device__ void block_scan_incl(int* buf, int n) {
 }
 
 // Single work-group: histogram, offsets, tile table, stable placement.
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __restrict__ ids, int P, int E,
-                                                               int tile_m, int32_t* __restrict__ counts,
-                                                               int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ sorted_pair,
-                                                               int32_t* __restrict__ tiles, int max_tiles,
-                                                               int32_t* __restrict__ ntiles) {
-  __shared__ int cnt[kMaxE];
-  __shared__ int scan[kMaxE];
-  __shared__ int tscan[kMaxE];
-  __shared__ int cursor[kMaxE];
-  __shared__ uint16_t wcnt[kPermWaves][kMaxE];
-
+// counts / offsets / tile table from the per-expert counts cnt[0..E) (LDS);
+// cursor (LDS, may be null) receives the exclusive offsets.  scan / tscan are
+// LDS scratch of kMaxE ints.  Called by every thread of the group.
+__device__ void permute_tables(const int* cnt, int* scan, int* tscan, int* cursor, int E, int tile_m,
+                               int32_t* counts, int32_t* offsets, int32_t* tiles, int max_tiles,
+                               int32_t* ntiles) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-
-  for (int i = tid; i < kMaxE; i += kPermThreads) cnt[i] = 0;
-  for (int i = tid; i < kPermWaves * kMaxE; i += kPermThreads) (&wcnt[0][0])[i] = 0;
-  __syncthreads();
-  for (int p = tid; p < P; p += kPermThreads) {
-    const int e = ids[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
   if (tid < E) {
     scan[tid] = cnt[tid];
     tscan[tid] = (cnt[tid] + tile_m - 1) / tile_m;
@@ -146,7 +129,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
     const int off = scan[tid] - c;
     counts[tid] = c;
     offsets[tid] = off;
-    cursor[tid] = off;
+    if (cursor) cursor[tid] = off;
     if (tid == E - 1) {
       offsets[E] = scan[tid];
       ntiles[0] = min(tscan[tid], max_tiles);
@@ -161,36 +144,69 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
     }
   }
   __syncthreads();
+}
 
-  // Stable placement, chunk by chunk in pair order (the next chunk's ids are
-  // loaded while this one is placed).
+// Stable rank of this thread's pair among the earlier pairs (lower thread
+// index) of the 1024-thread group with the same expert: within the wave from
+// ballots (one round per distinct expert), across waves from the per-wave
+// counts wcnt[w][e], which must be zero on entry and hold this chunk's counts
+// on return.  e = -1 marks an invalid pair (rank 0, not counted).
+__device__ int chunk_rank(int e, uint16_t (*wcnt)[kMaxE]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const bool valid = e >= 0;
+  int rank = 0;
+  uint64_t remaining = __ballot(valid);
+  while (remaining) {
+    const int leader = __ffsll((unsigned long long)remaining) - 1;  // wave-uniform
+    const int le = __builtin_amdgcn_readlane(e, leader);
+    const uint64_t m = __ballot(valid && e == le);
+    if (valid && e == le) {
+      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      rank = __popcll(m & lt);
+      if (lane == leader) wcnt[wave][e] = (uint16_t)__popcll(m);
+    }
+    remaining &= ~m;
+  }
+  __syncthreads();
+  if (valid)
+    for (int w = 0; w < wave; ++w) rank += wcnt[w][e];
+  return rank;
+}
+
+// Single work-group: histogram, tables, then stable placement chunk by chunk
+// in pair order (the next chunk's ids are loaded while one is placed).
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                               int tile_m, int32_t* __restrict__ counts,
+                                                               int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ sorted_pair,
+                                                               int32_t* __restrict__ tiles, int max_tiles,
+                                                               int32_t* __restrict__ ntiles) {
+  __shared__ int cnt[kMaxE];
+  __shared__ int scan[kMaxE];
+  __shared__ int tscan[kMaxE];
+  __shared__ int cursor[kMaxE];
+  __shared__ uint16_t wcnt[kPermWaves][kMaxE];
+
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kMaxE; i += kPermThreads) cnt[i] = 0;
+  for (int i = tid; i < kPermWaves * kMaxE; i += kPermThreads) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  for (int p = tid; p < P; p += kPermThreads) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  permute_tables(cnt, scan, tscan, cursor, E, tile_m, counts, offsets, tiles, max_tiles, ntiles);
+
   int e_next = (tid < P) ? ids[tid] : -1;
   for (int base = 0; base < P; base += kPermThreads) {
     const int p = base + tid;
     int e = e_next;
     e_next = (p + kPermThreads < P) ? ids[p + kPermThreads] : -1;
-    const bool valid = e >= 0 && e < E;
-    if (!valid) e = -1;
-    // rank among earlier lanes of this wave with the same expert
-    int rank = 0;
-    uint64_t remaining = __ballot(valid);
-    while (remaining) {
-      const int leader = __ffsll((unsigned long long)remaining) - 1;  // wave-uniform
-      const int le = __builtin_amdgcn_readlane(e, leader);
-      const uint64_t m = __ballot(valid && e == le);
-      if (valid && e == le) {
-        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        rank = __popcll(m & lt);
-        if (lane == leader) wcnt[wave][e] = (uint16_t)__popcll(m);
-      }
-      remaining &= ~m;
-    }
-    __syncthreads();
-    if (valid) {
-      int before = 0;
-      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
-      sorted_pair[cursor[e] + before + rank] = p;
-    }
+    if (!(e >= 0 && e < E)) e = -1;
+    const int rank = chunk_rank(e, wcnt);
+    if (e >= 0) sorted_pair[cursor[e] + rank] = p;
     __syncthreads();
     if (tid < E) {
       int add = 0;
@@ -202,6 +218,65 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
     }
     __syncthreads();
   }
+}
+
+// ---- multi-work-group path (P > 2 chunks and a workspace of
+// ceil(P / 1024) * E ints): per-chunk histograms, one scan group that turns
+// them into per-(chunk, expert) output bases and builds the tables, and one
+// placement group per chunk.  Same output as permute_kernel.
+
+__global__ __launch_bounds__(256) void perm_hist_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                        int32_t* __restrict__ hist) {
+  __shared__ int h[kMaxE];
+  for (int i = threadIdx.x; i < E; i += 256) h[i] = 0;
+  __syncthreads();
+  const int base = blockIdx.x * kPermThreads;
+  for (int i = threadIdx.x; i < kPermThreads; i += 256) {
+    const int p = base + i;
+    const int e = p < P ? ids[p] : -1;
+    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < E; i += 256) hist[(size_t)blockIdx.x * E + i] = h[i];
+}
+
+__global__ __launch_bounds__(kPermThreads) void perm_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E,
+                                                                 int tile_m, int32_t* __restrict__ counts,
+                                                                 int32_t* __restrict__ offsets,
+                                                                 int32_t* __restrict__ tiles, int max_tiles,
+                                                                 int32_t* __restrict__ ntiles) {
+  __shared__ int cnt[kMaxE];
+  __shared__ int scan[kMaxE];
+  __shared__ int tscan[kMaxE];
+  const int e = threadIdx.x;
+  if (e < E) {
+    int run = 0;  // exclusive prefix over the chunks, per expert
+    for (int c = 0; c < nchunks; ++c) {
+      const int v = hist[(size_t)c * E + e];
+      hist[(size_t)c * E + e] = run;
+      run += v;
+    }
+    cnt[e] = run;
+  }
+  __syncthreads();
+  permute_tables(cnt, scan, tscan, nullptr, E, tile_m, counts, offsets, tiles, max_tiles, ntiles);
+  if (e < E) {
+    const int off = scan[e] - cnt[e];
+    for (int c = 0; c < nchunks; ++c) hist[(size_t)c * E + e] += off;
+  }
+}
+
+__global__ __launch_bounds__(kPermThreads) void perm_place_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                                  const int32_t* __restrict__ base,
+                                                                  int32_t* __restrict__ sorted_pair) {
+  __shared__ uint16_t wcnt[kPermWaves][kMaxE];
+  for (int i = threadIdx.x; i < kPermWaves * E; i += kPermThreads) wcnt[i / E][i % E] = 0;
+  const int p = blockIdx.x * kPermThreads + threadIdx.x;
+  int e = p < P ? ids[p] : -1;
+  if (!(e >= 0 && e < E)) e = -1;
+  __syncthreads();
+  const int rank = chunk_rank(e, wcnt);
+  if (e >= 0) sorted_pair[base[(size_t)blockIdx.x * E + e] + rank] = p;
 }
 
 }  // namespace ferret
@@ -231,15 +306,33 @@ extern "C" int ferret_moe_tile_m(int num_pairs, int E) {
   return (E > 0 && num_pairs / E >= 32) ? 128 : 16;
 }
 
+// Workspace of the multi-work-group permutation (0: single work-group).
+size_t ferret_moe_permute_workspace(long long num_pairs, int E) {
+  const long long nchunks = (num_pairs + kPermThreads - 1) / kPermThreads;
+  return nchunks > 2 ? (size_t)nchunks * E * sizeof(int32_t) : 0;
+}
+
 extern "C" int ferret_moe_permute(const int32_t* ids, int T, int topk, int E, int tile_m, int32_t* counts,
                                   int32_t* offsets, int32_t* sorted_pair, int32_t* tiles, int max_tiles,
-                                  int32_t* ntiles, void* stream) {
+                                  int32_t* ntiles, void* ws, size_t ws_bytes, void* stream) {
   FERRET_REQUIRE(ids && counts && offsets && sorted_pair && tiles && ntiles, FERRET_ERR_NULL);
   FERRET_REQUIRE(T >= 0 && topk >= 1 && E >= 1 && E <= kMaxE && tile_m >= 1, FERRET_ERR_SHAPE);
   const long long P = (long long)T * topk;
   FERRET_REQUIRE(P <= (1ll << 22), FERRET_ERR_SHAPE);
   FERRET_REQUIRE(max_tiles >= ferret_moe_max_tiles((int)P, E, tile_m), FERRET_ERR_SHAPE);
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, (hipStream_t)stream, ids, (int)P, E,
-                     tile_m, counts, offsets, sorted_pair, tiles, max_tiles, ntiles);
+  const hipStream_t st = (hipStream_t)stream;
+  const size_t need = ferret_moe_permute_workspace(P, E);
+  if (need > 0 && ws != nullptr && ws_bytes >= need) {
+    const int nchunks = (int)((P + kPermThreads - 1) / kPermThreads);
+    int32_t* hist = static_cast<int32_t*>(ws);
+    hipLaunchKernelGGL(perm_hist_kernel, dim3(nchunks), dim3(256), 0, st, ids, (int)P, E, hist);
+    hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(kPermThreads), 0, st, hist, nchunks, E, tile_m, counts,
+                       offsets, tiles, max_tiles, ntiles);
+    hipLaunchKernelGGL(perm_place_kernel, dim3(nchunks), dim3(kPermThreads), 0, st, ids, (int)P, E,
+                       (const int32_t*)hist, sorted_pair);
+    return (int)hipGetLastError();
+  }
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, st, ids, (int)P, E, tile_m, counts, offsets,
+                     sorted_pair, tiles, max_tiles, ntiles);
   return (int)hipGetLastError();
 }

@@ -23,7 +23,8 @@ SIGNATURES = {
     "ferret_linear_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t, _vp]),
     "ferret_fp8_gemm_blockscale": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t, _vp]),
     "ferret_moe_route_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
-    "ferret_moe_permute": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "ferret_moe_permute": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                    _c_size_t, _vp]),
     "ferret_moe_max_tiles": (_c_int, [_c_int, _c_int, _c_int]),
     "ferret_moe_tile_m": (_c_int, [_c_int, _c_int]),
     "ferret_moe_w13_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -115,12 +115,22 @@ def tile_m_for(num_pairs: int, num_experts: int) -> int:
     return int(_lib.load().ferret_moe_tile_m(num_pairs, num_experts))
 
 
-def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int | None = None) -> Routing:
+def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int | None = None,
+                workspace: torch.Tensor | None = None) -> Routing:
+    """Stable expert-major permutation + tile table of the routed pairs.
+
+    Large P runs over several work-groups through a workspace of
+    ferret_workspace_bytes(4, P, 0, 0, E) bytes (taken from torch's caching
+    allocator unless one at least that large is passed).
+    """
     T, topk = ids.shape
     P = T * topk
     if tile_m is None:
         tile_m = tile_m_for(P, num_experts)
     L = _lib.load()
+    need = int(L.ferret_workspace_bytes(4, P, 0, 0, num_experts))
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=ids.device)
     max_tiles = max(1, int(L.ferret_moe_max_tiles(P, num_experts, tile_m)))
     dev = ids.device
     r = Routing(
@@ -132,7 +142,8 @@ def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int | None = None) 
         tile_m=tile_m, max_tiles=max_tiles, num_experts=num_experts, topk=topk, num_tokens=T)
     rc = L.ferret_moe_permute(_dev(ids, "ids", torch.int32, 2), T, topk, num_experts, tile_m,
                               r.counts.data_ptr(), r.offsets.data_ptr(), r.sorted_pair.data_ptr(),
-                              r.tiles.data_ptr(), max_tiles, r.ntiles.data_ptr(), _stream())
+                              r.tiles.data_ptr(), max_tiles, r.ntiles.data_ptr(),
+                              _dev(workspace, "workspace") if need else None, need, _stream())
     _lib.check("ferret_moe_permute", rc)
     return r
 

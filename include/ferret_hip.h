@@ -96,11 +96,14 @@ int ferret_moe_route_topk(const float* logits, int T, int E, int topk, int32_t* 
  * of expert 0 in ascending order, then expert 1, ...; ids outside [0,E) are
  * dropped), tiles[max_tiles*3] rows (expert, first sorted row, rows <= tile_m)
  * in expert order, ntiles[1].  max_tiles must be >= ferret_moe_max_tiles().
+ * `ws` (optional): with at least ferret_workspace_bytes(4, P, 0, 0, E) bytes
+ * the work is spread over one work-group per 1024 pairs (same output); with
+ * NULL one work-group does it all (fine for decode-sized P).
  * Requirements: P = T*topk <= 1<<22, E <= 1024.
  */
 int ferret_moe_permute(const int32_t* ids, int T, int topk, int E, int tile_m, int32_t* counts,
                        int32_t* offsets, int32_t* sorted_pair, int32_t* tiles, int max_tiles,
-                       int32_t* ntiles, void* stream);
+                       int32_t* ntiles, void* ws, size_t ws_bytes, void* stream);
 
 /* Upper bound on the tile count of ferret_moe_permute for P pairs. */
 int ferret_moe_max_tiles(int num_pairs, int E, int tile_m);
@@ -144,7 +147,7 @@ int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
 
 /* Workspace bytes an op can use (0 = none). op: 0 linear_bf16,
  * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
- * 3 moe_w13_w4a16. */
+ * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts). */
 size_t ferret_workspace_bytes(int op, int M, int N, int K, int E);
 
 #ifdef __cplusplus

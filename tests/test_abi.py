@@ -52,7 +52,9 @@ def test_argument_errors_are_returned_not_raised_without_gpu():
     assert L.ferret_linear_bf16(1, 1, None, 1, 1, 17, 128, None, 0, None) == -2
     assert L.ferret_fp8_gemm_blockscale(1, 1, 1, 1, 1, 4, 64, 100, None, 0, None) == -2
     assert L.ferret_moe_route_topk(1, 4, 2000, 8, 1, None, None) == -2
-    assert L.ferret_moe_permute(1, 4, 8, 16, 16, 1, 1, 1, 1, 0, 1, None) == -2
+    assert L.ferret_moe_permute(1, 4, 8, 16, 16, 1, 1, 1, 1, 0, 1, None, 0, None) == -2
+    assert L.ferret_workspace_bytes(4, 1024, 0, 0, 256) == 0          # one work-group
+    assert L.ferret_workspace_bytes(4, 32768, 0, 0, 256) == 32 * 256 * 4
     assert L.ferret_moe_w13_w4a16(1, 1, 1, 1, 1, 1, 10, 128, 4, 8, 16, 64, 256, 1, None) == -2
 
 

@@ -181,6 +181,34 @@ def test_permute_bit_exact(ops, T, k, E, tile_m, invalid):
     assert np.array_equal(rt.tiles.cpu().numpy()[:nt], tiles)
 
 
+@pytest.mark.parametrize("T,k,E,tile_m", [(3000, 8, 384, 16), (4096, 8, 256, 128), (2049, 1, 7, 128)])
+def test_permute_multi_group_matches_single_group(hip, ops, T, k, E, tile_m):
+    """The multi-work-group path (workspace given) and the one-group path (NULL) agree bit for bit."""
+    rng = np.random.default_rng(T * k + E)
+    ids_np = rng.integers(-1, E + 1, size=(T, k)).astype(np.int32)  # includes dropped ids
+    ids = torch.from_numpy(ids_np).cuda()
+    P = T * k
+    need = int(hip.ferret_workspace_bytes(4, P, 0, 0, E))
+    assert need > 0
+    with_ws = ops.moe_permute(ids, E, tile_m)          # takes the multi-group path
+    L = hip
+    max_tiles = with_ws.max_tiles
+    outs = [torch.full_like(t, -7) for t in (with_ws.counts, with_ws.offsets, with_ws.sorted_pair, with_ws.tiles,
+                                             with_ws.ntiles)]
+    rc = L.ferret_moe_permute(ids.data_ptr(), T, k, E, tile_m, outs[0].data_ptr(), outs[1].data_ptr(),
+                              outs[2].data_ptr(), outs[3].data_ptr(), max_tiles, outs[4].data_ptr(), None, 0,
+                              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    nt = int(with_ws.ntiles.item())
+    assert torch.equal(outs[0], with_ws.counts) and torch.equal(outs[1], with_ws.offsets)
+    n_valid = int(with_ws.offsets[E].item())
+    assert torch.equal(outs[2][:n_valid], with_ws.sorted_pair[:n_valid])
+    assert int(outs[4].item()) == nt and torch.equal(outs[3][:nt], with_ws.tiles[:nt])
+    counts, offsets, sp, tiles = oracle_routing(ids_np, E, tile_m)
+    assert np.array_equal(with_ws.sorted_pair.cpu().numpy()[: len(sp)], sp)
+
+
 # ------------------------------------------------------------------ MoE w13
 
 def _moe_fp8_small(T, E, N, K, topk, seed):
