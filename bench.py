@@ -380,7 +380,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD)
     ap.add_argument("--also", nargs="*", default=None,
-                    help="extra workloads measured in the same run (default: the decode sizes of the dense FP8 GEMM)")
+                    help="extra workloads measured in the same run (default with the default workload: all others)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--kernel-result", choices=sorted(FAMILIES), default=None)
@@ -397,7 +397,8 @@ def main(argv=None) -> int:
               "one GPU only (no collective or sharded step exists). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.also is None:
-        args.also = ["dsv3_fp8_M16", "dsv3_fp8_M128"] if args.workload == DEFAULT_WORKLOAD else []
+        args.also = [k for k in ("dsv3_fp8_M16", "dsv3_fp8_M128", "qwen3_gateup_M16", "dsv3_moe_w13_decode",
+                                 "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill")] if args.workload == DEFAULT_WORKLOAD else []
     import torch
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
