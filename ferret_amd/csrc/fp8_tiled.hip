@@ -154,9 +154,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   // instruction j (= w * TB_LD_PER_WAVE + i for wave w) fills stage bytes
   // j KB .. +1 KB: lane l -> row j*8 + l/8 of its part, LDS slot l%8 holding
   // global chunk (l%8) ^ key(row), so every instruction reads eight complete
-  // 128-B lines.  Weight rows are read with
-  // the non-temporal policy (streamed once per tile).  Addresses are a uniform
-  // base plus 32-bit per-lane offsets.
+  // 128-B lines.
   const uint8_t* wbase = p.b + (size_t)e * N * K;
   uint32_t goff[TB_LD_PER_WAVE];
 #pragma unroll
@@ -179,6 +177,15 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       goff[i] = (uint32_t)tok * (uint32_t)K + chunk * 16;
     }
   }
+  // Per-lane source of each load instruction (weights or tokens), so the
+  // stage copy is branch-free.  Both operands use the default cache policy:
+  // each is re-read by other tiles through L2.
+  const uint8_t* src[TB_LD_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
+    const int j = wave * TB_LD_PER_WAVE + i;
+    src[i] = (j < C::kWInstr ? wbase : p.a) + goff[i];
+  }
   // The last two waves also move the tile's 128 activation scales of the
   // K-step into the stage (4 bytes per lane): the main loop then issues no
   // other vector loads, so the vmcnt bookkeeping below is exact.
@@ -196,10 +203,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
       const int j = wave * TB_LD_PER_WAVE + i;  // uniform
       uint8_t* dst = stage + j * 1024;
-      if (j < C::kWInstr)
-        g2l_16_nt(wbase + (size_t)kb * TB_K + goff[i], dst);
-      else
-        g2l_16(p.a + (size_t)kb * TB_K + goff[i], dst);
+      g2l_16(src[i] + (size_t)kb * TB_K, dst);
     }
     if (sa_wave)
       __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
