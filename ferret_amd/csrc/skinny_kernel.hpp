@@ -49,22 +49,39 @@ constexpr int kRedBlock = 16 * kRedStride;  // floats per (wave, row block)
 // x & 0x0F0F0F0F through inline asm: hiding the known-zero bits from the
 // compiler keeps it converting bytes with v_cvt_f32_ubyte{0..3} (one op each)
 // instead of extracting every nibble with v_bfe_u32 first.
-__device__ __forceinline__ uint32_t nibbles_as_bytes(uint32_t x) {
-  uint32_t r;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x));
-  return r;
+// Per-group constants of the INT4 dequant (group scale s, a bf16 value).
+struct Int4Scale {
+  float s, s16, c1, c2;
+};
+__device__ __forceinline__ Int4Scale int4_scale(float s) {
+  return Int4Scale{s, s * 0.0625f, -1032.0f * s, -72.0f * s};
 }
 
-// INT4 word (8 nibbles, low first, offset-8) -> 8 bf16 = RNE(float(q - 8) * s).
-// fma(q, s, -8s) is exact: (q - 8) * s needs <= 12 significant bits.
-__device__ __forceinline__ u32x4 dequant_int4x8(uint32_t w, float s, float ns8) {
-  const uint32_t lo = nibbles_as_bytes(w);
-  const uint32_t hi = nibbles_as_bytes(w >> 4);
+// INT4 word (8 nibbles q0..q7, low first, offset-8) -> 8 bf16 = RNE(float(q - 8) * s).
+// The nibbles are placed in fp16 mantissas under the exponent of 1024 with no
+// shift: 0x6400 | q reads 1024 + q, 0x6400 | (q << 4) reads 1024 + 16 q.  One
+// mixed fma per weight then forms (1024 + q) s - 1032 s, resp.
+// (1024 + 16 q)(s / 16) - 72 s: the fma rounds the exact value (q - 8) s once,
+// which needs <= 12 significant bits and so is exact in fp32 (as are 1032 s,
+// 72 s and s / 16 for a bf16 s), and the bf16 pack rounds it to nearest even.
+__device__ __forceinline__ u32x4 dequant_int4x8(uint32_t w, const Int4Scale& k) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  // The three constants as register values (VOP3 takes no literal here), so
+  // each mask-and-merge is one v_and_or_b32; the asm is CSE'd and hoisted.
+  uint32_t magic, m_lo, m_hi;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  asm("s_mov_b32 %0, 0x000F000F" : "=s"(m_lo));
+  asm("s_mov_b32 %0, 0x00F000F0" : "=s"(m_hi));
+  const uint32_t w8 = w >> 8;
+  const h2 t0 = __builtin_bit_cast(h2, (w & m_lo) | magic);   // q0, q4
+  const h2 t1 = __builtin_bit_cast(h2, (w & m_hi) | magic);   // q1, q5 (x16)
+  const h2 t2 = __builtin_bit_cast(h2, (w8 & m_lo) | magic);  // q2, q6
+  const h2 t3 = __builtin_bit_cast(h2, (w8 & m_hi) | magic);  // q3, q7 (x16)
   u32x4 d;
-  d[0] = pack_bf16x2(fmaf((float)(lo & 0xffu), s, ns8), fmaf((float)(hi & 0xffu), s, ns8));
-  d[1] = pack_bf16x2(fmaf((float)((lo >> 8) & 0xffu), s, ns8), fmaf((float)((hi >> 8) & 0xffu), s, ns8));
-  d[2] = pack_bf16x2(fmaf((float)((lo >> 16) & 0xffu), s, ns8), fmaf((float)((hi >> 16) & 0xffu), s, ns8));
-  d[3] = pack_bf16x2(fmaf((float)(lo >> 24), s, ns8), fmaf((float)(hi >> 24), s, ns8));
+  d[0] = pack_bf16x2(fmaf((float)t0.x, k.s, k.c1), fmaf((float)t1.x, k.s16, k.c2));
+  d[1] = pack_bf16x2(fmaf((float)t2.x, k.s, k.c1), fmaf((float)t3.x, k.s16, k.c2));
+  d[2] = pack_bf16x2(fmaf((float)t0.y, k.s, k.c1), fmaf((float)t1.y, k.s16, k.c2));
+  d[3] = pack_bf16x2(fmaf((float)t2.y, k.s, k.c1), fmaf((float)t3.y, k.s16, k.c2));
   return d;
 }
 
@@ -191,10 +208,10 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const float sc = bf16_bits_to_f32(s4[slot][rb]);
-        const float ns8 = -8.0f * sc;
+        const Int4Scale ks4 = int4_scale(sc);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(wbuf[slot][rb][0][j], sc, ns8), xbuf[slot][j], acc[rb]);
+          acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(wbuf[slot][rb][0][j], ks4), xbuf[slot][j], acc[rb]);
       }
     }
   }

@@ -106,6 +106,15 @@ __device__ __forceinline__ void static_for(Fn&& f) {
 // s_waitcnt lgkmcnt(0) only (LDS writes done before a barrier).
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
+// The weight fragments of one K-step held by a lane: 16-byte LDS chunks per
+// 16-row block (bf16 4, fp8 2, int4 1) and the block's scale (fp8 weight-block
+// scale; int4 group scale).
+template <int F, int RB>
+struct StepFrag {
+  u32x4 w[RB][F == kBF16 ? 4 : (F == kFP8 ? 2 : 1)];
+  float sv[RB];
+};
+
 template <int F, int EPI, int RB, int NW, int KS, int D>
 __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int dense_tiles) {
   using C = StreamCfg<F, RB, NW, KS, D>;
@@ -284,46 +293,73 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     }
 
     const uint8_t* sb_unit = sclbuf + (u & 1) * C::kSclBuf;
-    static_for<0, KS>([&](auto sc) {
-      constexpr int s = decltype(sc)::value;
-      const int it = (u - u_begin) * KS + s;
-      // Wait for this item's stage (items issued after it may stay in flight).
-      wait_items<L, SI, KS, s, D - 1>(min(D - 1, n_items - 1 - it));
-      __builtin_amdgcn_sched_barrier(0);
-      const int slot = it % D;
+    // One K-step's weight fragments (and their scales), read from its stage.
+    auto load_frag = [&](StepFrag<F, RB>& fr, int slot, int s) {
       const uint8_t* st = ring + slot * C::kStage;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const uint8_t* blk = st + rb * 16 * ROWB + r * ROWB;
         if constexpr (F == kBF16) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const u32x4 wf = *reinterpret_cast<const u32x4*>(blk + (sw_bf16(r, 4 * g + j) << 4));
-            acc[rb] = mfma_bf16_16x16x32(wf, xv[s][j], acc[rb]);
-          }
+          for (int j = 0; j < 4; ++j) fr.w[rb][j] = *reinterpret_cast<const u32x4*>(blk + (sw_bf16(r, 4 * g + j) << 4));
         } else if constexpr (F == kFP8) {
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g) << 4));
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g + 1) << 4));
-          const f32x4 part = fp8_block_16x16x128(lo, hi, xv[s][0], xv[s][1]);
-          const float sb = *reinterpret_cast<const float*>(st + C::kWBytes + 4 * rb);
-          const float sc = sx[s] * sb;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(part[i], sc, acc[rb][i]);
+          fr.w[rb][0] = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g) << 4));
+          fr.w[rb][1] = *reinterpret_cast<const u32x4*>(blk + (sw_fp8(r, 2 * g + 1) << 4));
+          fr.sv[rb] = *reinterpret_cast<const float*>(st + C::kWBytes + 4 * rb);
         } else {
-          const u32x4 wq = *reinterpret_cast<const u32x4*>(blk + (sw_int4(r, g) << 4));
-          const uint16_t sbits = *reinterpret_cast<const uint16_t*>(
-              sb_unit + (rb * 16 + r) * (SCH * 16) + (s_start - s_a0) + s * 8 + g * 2);
-          const float sc = bf16_bits_to_f32(sbits);
-          const float ns8 = -8.0f * sc;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(wq[j], sc, ns8), xv[s][j], acc[rb]);
+          fr.w[rb][0] = *reinterpret_cast<const u32x4*>(blk + (sw_int4(r, g) << 4));
+          fr.sv[rb] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(
+              sb_unit + (rb * 16 + r) * (SCH * 16) + (s_start - s_a0) + s * 8 + g * 2));
         }
       }
+    };
+    auto compute = [&](const StepFrag<F, RB>& fr, auto sc) {
+      constexpr int s = decltype(sc)::value;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if constexpr (F == kBF16) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[rb] = mfma_bf16_16x16x32(fr.w[rb][j], xv[s][j], acc[rb]);
+        } else if constexpr (F == kFP8) {
+          const f32x4 part = fp8_block_16x16x128(fr.w[rb][0], fr.w[rb][1], xv[s][0], xv[s][1]);
+          const float scl = sx[s] * fr.sv[rb];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(part[i], scl, acc[rb][i]);
+        } else {
+          const Int4Scale ks4 = int4_scale(fr.sv[rb]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[rb] = mfma_bf16_16x16x32(dequant_int4x8(fr.w[rb][0][j], ks4), xv[s][j], acc[rb]);
+        }
+      }
+    };
+
+    // Software pipeline over the unit's K-steps: the fragments of step s+1 are
+    // read from LDS while step s computes, so the LDS latency hides behind the
+    // MFMA/dequant work of the same wave.
+    StepFrag<F, RB> cur;
+    {
+      const int it0 = (u - u_begin) * KS;
+      wait_items<L, SI, KS, 0, D - 1>(min(D - 1, n_items - 1 - it0));
       __builtin_amdgcn_sched_barrier(0);
-      // Refill the slot just read (its fragments are in registers by now).
-      if (it + D < n_items) issue(slot);
+      load_frag(cur, it0 % D, 0);
+    }
+    static_for<0, KS>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
+      const int it = (u - u_begin) * KS + s;
+      StepFrag<F, RB> nxt;
+      if constexpr (s + 1 < KS) {
+        // Wait for step s+1's stage (items issued after it may stay in flight).
+        wait_items<L, SI, KS, s + 1, (D >= 2 ? D - 2 : 0)>(min(D - 2, n_items - 2 - it));
+        __builtin_amdgcn_sched_barrier(0);
+        load_frag(nxt, (it + 1) % D, s + 1);
+      }
+      compute(cur, sc);
       __builtin_amdgcn_sched_barrier(0);
+      // Refill the slot of step s (its fragments were consumed above).
+      if (it + D < n_items) issue(it % D);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (s + 1 < KS) cur = nxt;
     });
 
     // ---- unit end: cross-wave K reduction through LDS, then the epilogue.
