@@ -59,8 +59,11 @@ struct StreamCfg {
   // INT4: the group scales of a unit (RB * 16 rows x this wave's KS K-steps,
   // 8 B per row and K-step) are copied once per unit as whole 16-B chunks:
   // kSclCh chunks per row cover the wave's (8-B aligned) span, double-buffered
-  // by unit parity; kSclLoads DMA ops (16 B per lane) per unit.
-  static constexpr int kSclCh = (KS * 8 + 8 + 15) / 16;
+  // by unit parity; kSclLoads DMA ops (16 B per lane) per unit.  kSclCh is
+  // odd (a spare chunk pads an even count): the 16 rows one read touches then
+  // sit at 8 distinct 16-B bank groups, two rows each, where an even row
+  // stride of 64 B would pile 8 rows onto each of two groups.
+  static constexpr int kSclCh = ((KS * 8 + 8 + 15) / 16) | 1;
   static constexpr int kSclBuf = RB * 16 * kSclCh * 16;
   static constexpr int kSclLoads = F == kINT4 ? (RB * 16 * kSclCh + 63) / 64 : 0;
   static constexpr int kScl = F == kINT4 ? 2 * kSclBuf : 0;            // per wave
@@ -73,9 +76,12 @@ struct StreamCfg {
 };
 
 // Chunk slot of global 16-byte chunk c of LDS row `row` (per row width).
+// A ds_read_b128 is served 8 lanes at a time over 128 B of banks, so the 8
+// rows that lanes r..r+7 read (same chunk c) must land on 8 distinct 16-B
+// bank groups; with a 64-B int4 row that takes the key (row >> 1) & 3.
 __device__ __forceinline__ int sw_bf16(int row, int c) { return c ^ (((row & 7) << 1) | ((row >> 3) & 1)); }
 __device__ __forceinline__ int sw_fp8(int row, int c) { return c ^ ((row & 7) ^ ((row >> 3) & 1)); }
-__device__ __forceinline__ int sw_int4(int row, int c) { return c ^ ((row >> 2) & 3); }
+__device__ __forceinline__ int sw_int4(int row, int c) { return c ^ ((row >> 1) & 3); }
 
 // Wait until item S of a unit (K-step S of KS) has landed, while the
 // min(n, N) items issued after it may stay in flight: each item is L DMA ops,
