@@ -208,6 +208,17 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     if (sa_wave)
       __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
   };
+  // Instruction i of this wave's share of stage `step` (i == TB_LD_PER_WAVE:
+  // the activation scales, scale waves only).
+  auto issue_one = [&](int step, int i) {
+    uint8_t* stage = lds + (step % TB_NS) * TB_STAGE;
+    const int kb = kb0 + step;
+    if (i < TB_LD_PER_WAVE) {
+      g2l_16(src[i] + (size_t)kb * TB_K, stage + (wave * TB_LD_PER_WAVE + i) * 1024);
+    } else if (sa_wave) {
+      __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
+    }
+  };
   // This thread's copy of stage kb is complete once at most `younger` later
   // stages remain in flight (vector-memory ops per thread and stage:
   // TB_LD_PER_WAVE, plus one for the scale waves).
@@ -252,10 +263,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Prologue: stages 0 .. NS-2 in flight.
+  // Prologue: stages 0 .. NS-2 in flight (and stage NS-1 too from the
+  // token-half-1 waves of the staggered loop, see below).
 #pragma unroll
   for (int s = 0; s < TB_NS - 1; ++s)
     if (s < nsteps) issue_stage(s);
+  if (PP && wm == 1 && TB_NS - 1 < nsteps) issue_stage(TB_NS - 1);
 
   // One K-step is two phases: X (LDS fragment reads + e4m3 -> bf16 widening,
   // VALU only) and Y (the MFMAs + the scale folds).  Fragments widened by X
@@ -315,6 +328,32 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       }
     }
   };
+  // Phase Y with this wave's share of the copy of stage `istep` (istep < 0:
+  // none) spread over its MFMA blocks, one instruction after every second
+  // block: issued in one burst after a barrier, the eight waves' copies queue
+  // behind each other and stall the later waves for most of a phase.
+  auto phase_y_copy = [&](auto mic, int istep) {
+    constexpr int MI = decltype(mic)::value;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const float sbv = (SILU && ni >= 2) ? sbu : sbg;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        f32x4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[ni][j], abf[mi][j], part);
+        const float sc = sa_v[mi] * sbv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
+        const int b = ni * MI + mi;
+        if (b % 2 == 1 && b / 2 <= TB_LD_PER_WAVE && istep >= 0) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_one(istep, b / 2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
   // One K-step of the single-phase loop.  The interleave hint asks the
   // scheduler for its single-wave MFMA order (LDS reads and VALU widening
   // slotted between MFMAs): ~7% faster than its default order on the
@@ -339,26 +378,35 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   };
 
   if constexpr (PP) {
-    // Ping-pong (full token tiles): waves w and w + WN share a SIMD (work-group
-    // waves are dealt to the four SIMDs round-robin), so the token-half-0 waves
-    // run X while their SIMD partners run Y of the previous K-step, and vice
-    // versa; the MFMAs of one wave overlap the VALU widening of the other.  Both
-    // halves pass the same 2 * nsteps + 1 barriers.
+    // Staggered halves (full token tiles): waves w and w + WN share a SIMD
+    // (work-group waves are dealt to the four SIMDs round-robin).  Between
+    // the barriers that open K-steps s and s+1 the token-half-0 waves run
+    // X(s) Y(s) and the token-half-1 waves Y(s-1) X(s), so one wave's MFMAs
+    // overlap its partner's VALU widening; both halves pass the same
+    // nsteps + 1 barriers, one per K-step.  Stage refills ride in the Y
+    // phases: half 0 refills stage s+2 in Y(s) (the slot of stage s-1, read
+    // by every wave before the barrier opening s), half 1 refills stage s+3
+    // in Y(s) (the slot of stage s, read by every wave before the barrier
+    // opening s+1, which precedes its Y(s)).  At each barrier a wave thus has
+    // at most one younger stage in flight, as wait_stage assumes; half 1
+    // issued stages 0..2 up front and waits for 0 and 1 at the first barrier.
+    auto open_wait = [&](int step) {
+      if (step < nsteps) wait_stage(min(nsteps - 1 - step, TB_NS - 2));
+      barrier();
+    };
     if (wm == 0) {
       for (int step = 0; step < nsteps; ++step) {
-        open_step(step);
+        open_wait(step);
         phase_x(IntC<4>{}, step);
-        barrier();
-        phase_y(IntC<4>{});
+        phase_y_copy(IntC<4>{}, step + TB_NS - 1 < nsteps ? step + TB_NS - 1 : -1);
       }
-      open_step(nsteps);
+      open_wait(nsteps);
     } else {
-      open_step(0);
+      open_wait(0);
       for (int step = 0; step < nsteps; ++step) {
-        barrier();
         phase_x(IntC<4>{}, step);
-        open_step(step + 1);
-        phase_y(IntC<4>{});
+        open_wait(step + 1);
+        phase_y_copy(IntC<4>{}, step + TB_NS < nsteps ? step + TB_NS : -1);
       }
     }
   } else {

@@ -123,6 +123,22 @@ def test_fp8_gemm_workspace_and_plain_paths(hip, ops, M, N, K):
         assert_gemm_close(bf16_out(c), ref, f"fp8 {tag} M={M}")
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 256, 128), (256, 256, 256), (384, 512, 384), (512, 256, 640)])
+def test_fp8_gemm_staggered_short_k(hip, M, N, K):
+    """Full 128-row token tiles without a workspace take the staggered
+    two-half loop; K of 1, 2, 3 and 5 K-steps covers its prologue (three
+    stages in flight for one half) and its last-stage waits."""
+    _say(f"fp8_gemm staggered M={M} N={N} K={K}")
+    a, sa, b, sb = _fp8_inputs(M, N, K, seed=11 * M + K)
+    ref = G.fp8_blockscale_gemm(codes8(a), f32(sa), codes8(b), f32(sb))
+    c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    rc = hip.ferret_fp8_gemm_blockscale(a.data_ptr(), sa.data_ptr(), b.data_ptr(), sb.data_ptr(), c.data_ptr(),
+                                        M, N, K, None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    assert_gemm_close(bf16_out(c), ref, f"fp8 staggered M={M} K={K}")
+
+
 def test_fp8_gemm_power_of_two_scales_exactish(ops):
     """Small-integer e4m3 values with power-of-two scales: exact sums, only the bf16 rounding differs."""
     M, N, K = 32, 256, 512
