@@ -196,18 +196,6 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
     sa_src = p.sa + (size_t)tok * nkb;
   }
-  auto issue_stage = [&](int step) {
-    uint8_t* stage = lds + (step % TB_NS) * TB_STAGE;
-    const int kb = kb0 + step;
-#pragma unroll
-    for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
-      const int j = wave * TB_LD_PER_WAVE + i;  // uniform
-      uint8_t* dst = stage + j * 1024;
-      g2l_16(src[i] + (size_t)kb * TB_K, dst);
-    }
-    if (sa_wave)
-      __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
-  };
   // Instruction i of this wave's share of stage `step` (i == TB_LD_PER_WAVE:
   // the activation scales, scale waves only).
   auto issue_one = [&](int step, int i) {
@@ -218,6 +206,10 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     } else if (sa_wave) {
       __builtin_amdgcn_global_load_lds(sa_src + kb, stage + TB_SA_OFF + (wave - (TB_WAVES - 2)) * 256, 4, 0, 0);
     }
+  };
+  auto issue_stage = [&](int step) {
+#pragma unroll
+    for (int i = 0; i <= TB_LD_PER_WAVE; ++i) issue_one(step, i);
   };
   // This thread's copy of stage kb is complete once at most `younger` later
   // stages remain in flight (vector-memory ops per thread and stage:
@@ -268,7 +260,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
   for (int s = 0; s < TB_NS - 1; ++s)
     if (s < nsteps) issue_stage(s);
-  if (PP && wm == 1 && TB_NS - 1 < nsteps) issue_stage(TB_NS - 1);
+  if (wm == 1 && TB_NS - 1 < nsteps) issue_stage(TB_NS - 1);
 
   // One K-step is two phases: X (LDS fragment reads + e4m3 -> bf16 widening,
   // VALU only) and Y (the MFMAs + the scale folds).  Fragments widened by X
@@ -312,28 +304,20 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       wbf[ni][3] = e4m3x8_to_bf16x8(hi[2], hi[3]);
     }
   };
-  auto phase_y = [&](auto mic) {
-    constexpr int MI = decltype(mic)::value;
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-      const float sbv = (SILU && ni >= 2) ? sbu : sbg;
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi) {
-        f32x4 part = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[ni][j], abf[mi][j], part);
-        const float sc = sa_v[mi] * sbv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
-      }
-    }
-  };
   // Phase Y with this wave's share of the copy of stage `istep` (istep < 0:
-  // none) spread over its MFMA blocks, one instruction after every second
-  // block: issued in one burst after a barrier, the eight waves' copies queue
-  // behind each other and stall the later waves for most of a phase.
+  // none) spread over its MFMA blocks: instruction i goes after block 2i+1
+  // (or the last block; with no blocks all go at once).  Issued in one burst
+  // after a barrier, the eight waves' copies queue behind each other and
+  // stall the later waves for most of a phase.
   auto phase_y_copy = [&](auto mic, int istep) {
     constexpr int MI = decltype(mic)::value;
+    constexpr int NB = 4 * MI;
+    if constexpr (NB == 0) {
+      if (istep >= 0) {
+#pragma unroll
+        for (int i = 0; i <= TB_LD_PER_WAVE; ++i) issue_one(istep, i);
+      }
+    }
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       const float sbv = (SILU && ni >= 2) ? sbu : sbg;
@@ -346,84 +330,67 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
         const int b = ni * MI + mi;
-        if (b % 2 == 1 && b / 2 <= TB_LD_PER_WAVE && istep >= 0) {
-          __builtin_amdgcn_sched_barrier(0);
-          issue_one(istep, b / 2);
-          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i <= TB_LD_PER_WAVE; ++i) {
+          if (min(2 * i + 1, NB - 1) == b && istep >= 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue_one(istep, i);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     }
-  };
-  // One K-step of the single-phase loop.  The interleave hint asks the
-  // scheduler for its single-wave MFMA order (LDS reads and VALU widening
-  // slotted between MFMAs): ~7% faster than its default order on the
-  // 4096 x 4096 x 7168 GEMM.
-  auto step_xy = [&](auto mic, int step) {
-    phase_x(mic, step);
-    phase_y(mic);
-    __builtin_amdgcn_iglp_opt(1);
   };
   auto barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Barrier that opens K-step `step`: this thread's copy of the stage is
-  // complete before it, every wave's after it; the ring slot refilled right
-  // after it (stage step-1's) has been read by every wave by then.
-  auto open_step = [&](int step) {
-    if (step < nsteps) wait_stage(min(nsteps - 1 - step, TB_NS - 2));
-    barrier();
-    if (step + TB_NS - 1 < nsteps) issue_stage(step + TB_NS - 1);
-  };
-
-  if constexpr (PP) {
-    // Staggered halves (full token tiles): waves w and w + WN share a SIMD
-    // (work-group waves are dealt to the four SIMDs round-robin).  Between
-    // the barriers that open K-steps s and s+1 the token-half-0 waves run
-    // X(s) Y(s) and the token-half-1 waves Y(s-1) X(s), so one wave's MFMAs
-    // overlap its partner's VALU widening; both halves pass the same
-    // nsteps + 1 barriers, one per K-step.  Stage refills ride in the Y
-    // phases: half 0 refills stage s+2 in Y(s) (the slot of stage s-1, read
-    // by every wave before the barrier opening s), half 1 refills stage s+3
-    // in Y(s) (the slot of stage s, read by every wave before the barrier
-    // opening s+1, which precedes its Y(s)).  At each barrier a wave thus has
-    // at most one younger stage in flight, as wait_stage assumes; half 1
-    // issued stages 0..2 up front and waits for 0 and 1 at the first barrier.
+  {
+    // Staggered halves: waves w and w + WN share a SIMD (work-group waves are
+    // dealt to the four SIMDs round-robin).  Between the barriers that open
+    // K-steps s and s+1 the token-half-0 waves run X(s) Y(s) and the
+    // token-half-1 waves Y(s-1) X(s), so one wave's MFMAs overlap its
+    // partner's VALU widening; both halves pass the same nsteps + 1 barriers,
+    // one per K-step.  Stage refills ride in the Y phases: half 0 refills
+    // stage s+2 in Y(s) (the slot of stage s-1, read by every wave before the
+    // barrier opening s), half 1 refills stage s+3 in Y(s) (the slot of stage
+    // s, read by every wave before the barrier opening s+1, which precedes
+    // its Y(s)).  At each barrier a wave thus has at most one younger stage in
+    // flight, as wait_stage assumes; half 1 issued stages 0..2 up front and
+    // waits for 0 and 1 at the first barrier.  MI, the number of 16-token
+    // sub-tiles of the wave that hold tokens (uniform per wave), picks the
+    // loop instance: a partial tile of a grouped GEMM skips the empty ones.
     auto open_wait = [&](int step) {
       if (step < nsteps) wait_stage(min(nsteps - 1 - step, TB_NS - 2));
       barrier();
     };
-    if (wm == 0) {
+    auto half0 = [&](auto mic) {
       for (int step = 0; step < nsteps; ++step) {
         open_wait(step);
-        phase_x(IntC<4>{}, step);
-        phase_y_copy(IntC<4>{}, step + TB_NS - 1 < nsteps ? step + TB_NS - 1 : -1);
+        if constexpr (decltype(mic)::value > 0) phase_x(mic, step);
+        phase_y_copy(mic, step + TB_NS - 1 < nsteps ? step + TB_NS - 1 : -1);
       }
       open_wait(nsteps);
-    } else {
+    };
+    auto half1 = [&](auto mic) {
       open_wait(0);
       for (int step = 0; step < nsteps; ++step) {
-        phase_x(IntC<4>{}, step);
+        if constexpr (decltype(mic)::value > 0) phase_x(mic, step);
         open_wait(step + 1);
-        phase_y_copy(IntC<4>{}, step + TB_NS < nsteps ? step + TB_NS : -1);
-      }
-    }
-  } else {
-    // 16-token sub-tiles of this wave holding tokens (uniform per wave); one
-    // K-loop per count, so that each is scheduled for its own MI.
-    auto k_loop = [&](auto mic) {
-      for (int step = 0; step < nsteps; ++step) {
-        open_step(step);
-        if constexpr (decltype(mic)::value > 0) step_xy(mic, step);
+        phase_y_copy(mic, step + TB_NS < nsteps ? step + TB_NS : -1);
       }
     };
-    switch (max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
-      case 4: k_loop(IntC<4>{}); break;
-      case 3: k_loop(IntC<3>{}); break;
-      case 2: k_loop(IntC<2>{}); break;
-      case 1: k_loop(IntC<1>{}); break;
-      default: k_loop(IntC<0>{}); break;
+    auto run = [&](auto mic) {
+      if (wm == 0) half0(mic);
+      else half1(mic);
+    };
+    switch (PP ? 4 : max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
+      case 4: run(IntC<4>{}); break;
+      case 3: run(IntC<3>{}); break;
+      case 2: run(IntC<2>{}); break;
+      case 1: run(IntC<1>{}); break;
+      default: run(IntC<0>{}); break;
     }
   }
 
