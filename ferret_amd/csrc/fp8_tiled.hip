@@ -15,17 +15,18 @@
 // Work-group (large M): 512 threads = 8 waves (4 along weight rows x 2 along
 // tokens, two per SIMD so one wave's conversions overlap the other's MFMAs),
 // tile 256 weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
-// Small M (<= 256) with a workspace: 64 x 128 tiles (2 waves) over K ranges
+// Small M (<= 256) with a workspace: 128 x 128 tiles (4 waves) over K ranges
 // (split-K), fp32 partials summed in split order by a reduce kernel.
 // Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
 // staging) through a 3-stage ring; every load instruction reads complete
 // 128-byte lines; LDS rows of 128 B have their 16-byte chunk index
 // XOR-swizzled so the MFMA fragment reads are bank-conflict free.
-// Per K-step a wave widens its fragments (128 v_cvt_scalef32_pk_bf16_fp8) and
-// issues 64 MFMAs and 64 scale folds.  With full token tiles the two waves of
-// a SIMD run these halves out of phase (ping-pong, two barriers per K-step);
-// a partial tile (grouped GEMM) instead runs one barrier per K-step and skips
-// the MFMAs and widening of its empty 16-token sub-tiles.
+// Per K-step a wave widens its fragments (128 v_cvt_scalef32_pk_bf16_fp8:
+// phase X) and issues 64 MFMAs and 64 scale folds (phase Y).  The two token
+// halves of the tile run X and Y out of phase (one barrier per K-step), so the
+// two waves of a SIMD overlap one's MFMAs with the other's widening; the stage
+// refills are spread through the Y phases.  A partial tile (grouped GEMM)
+// skips the MFMAs and widening of its empty 16-token sub-tiles.
 //
 // Reference counterparts: fp8_gemm<BN,NS> (v002:61-249) and
 // grouped_fp8_gemm_bs<BN,NS> (examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-335),
@@ -39,7 +40,7 @@ constexpr int TB_M = 128;  // tokens per work-group (two token waves carry the 1
 
 // Tile geometry: WN waves along the weight rows (64 rows each) x 2 waves along
 // the tokens (64 each).  WN = 4: 256 x 128 tile, 8 waves (two per SIMD) for
-// large M; WN = 1: 64 x 128 tile, 2 waves, used with split-K for small M.
+// large M; WN = 2: 128 x 128 tile, 4 waves, used with split-K for small M.
 template <int WN>
 struct TileCfg {
   static constexpr int kWN = WN;
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-template <bool SILU, int WN, bool SPLIT, bool PP>
+template <bool SILU, int WN, bool SPLIT, bool FULL>
 __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   using C = TileCfg<WN>;
   constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       if (wm == 0) half0(mic);
       else half1(mic);
     };
-    switch (PP ? 4 : max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
+    switch (FULL ? 4 : max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
       case 4: run(IntC<4>{}); break;
       case 3: run(IntC<3>{}); break;
       case 2: run(IntC<2>{}); break;
@@ -432,12 +433,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
-template <bool SILU, int WN, bool SPLIT, bool PP>
+template <bool SILU, int WN, bool SPLIT, bool FULL>
 static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
   using C = TileCfg<WN>;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT, PP>,
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT, FULL>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
-  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT, PP>), grid, dim3(C::kThreads), C::kLds, st, p);
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT, FULL>), grid, dim3(C::kThreads), C::kLds, st, p);
   return (int)hipGetLastError();
 }
 
@@ -450,9 +451,6 @@ static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
 #endif
 #ifndef SPLITK_TARGET
 #define SPLITK_TARGET 256
-#endif
-#ifndef SPLITK_PP
-#define SPLITK_PP false
 #endif
 static int splitk_splits(int M, int N, int K) {
   if (M > 256 || N % (64 * SPLITK_WN) != 0) return 1;
@@ -488,15 +486,17 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     const int used = (nkb + p.k_steps - 1) / p.k_steps;  // splits actually holding K-steps
     p.partial = static_cast<float*>(ws);
     p.n_blocks = N / (64 * SPLITK_WN);
-    const int rc = launch_tiled<false, SPLITK_WN, true, SPLITK_PP>(p, dim3(p.n_blocks * p.m_blocks, used), st);
+    const dim3 grid(p.n_blocks * p.m_blocks, used);
+    const int rc = M % TB_M == 0 ? launch_tiled<false, SPLITK_WN, true, true>(p, grid, st)
+                                 : launch_tiled<false, SPLITK_WN, true, false>(p, grid, st);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
                        static_cast<uint16_t*>(c));
     return (int)hipGetLastError();
   }
-  // Dense tiles: ping-pong when every token tile is full (M % 128 == 0),
-  // else the single-phase loop, which skips a partial tile's empty sub-tiles.
+  // Dense tiles: with every token tile full (M % 128 == 0) the kernel skips
+  // the per-wave count of occupied 16-token sub-tiles.
   p.n_blocks = (N + 255) / 256;
   if (M % TB_M == 0) return launch_tiled<false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st);
   return launch_tiled<false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st);
