@@ -16,6 +16,13 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
                              const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
                              int max_tiles, int topk, int N, int K, void* out, hipStream_t st);
 
+int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, const float* sw,
+                             const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                             int max_tiles, int N, int K, void* out, hipStream_t st);
+int ferret_moe_w2_fp8_tiled(const void* h, const float* sh, const void* w, const float* sw,
+                            const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                            int max_tiles, int N, int K, void* out, hipStream_t st);
+
 extern "C" const char* ferret_version(void) { return "ferret-hip 0.1.0 gfx950"; }
 
 extern "C" const char* ferret_error_string(int code) {
@@ -60,5 +67,20 @@ extern "C" int ferret_moe_w13_fp8(const void* x, const float* sx, const void* w,
   if (tile_m == 128)
     return ferret_moe_w13_fp8_tiled(x, sx, w, sw, sorted_pair, tiles, ntiles, max_tiles, topk, N, K, out,
                                     (hipStream_t)stream);
+  return FERRET_ERR_SHAPE;
+}
+
+extern "C" int ferret_moe_w2_fp8(const void* h, const float* sh, const void* w, const float* sw,
+                                 const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                                 int max_tiles, int tile_m, int P, int E, int N, int K, void* out, void* stream) {
+  FERRET_REQUIRE(h && sh && w && sw && sorted_pair && tiles && ntiles && out, FERRET_ERR_NULL);
+  FERRET_REQUIRE(P >= 1 && E >= 1 && max_tiles >= 0, FERRET_ERR_SHAPE);
+  FERRET_REQUIRE(N % 128 == 0 && N >= 128 && K % 128 == 0 && K >= 128 && K / 128 <= 128, FERRET_ERR_SHAPE);
+  if (tile_m == 16)
+    return ferret_moe_w2_fp8_skinny(h, sh, w, sw, sorted_pair, tiles, ntiles, max_tiles, N, K, out,
+                                    (hipStream_t)stream);
+  if (tile_m == 128)
+    return ferret_moe_w2_fp8_tiled(h, sh, w, sw, sorted_pair, tiles, ntiles, max_tiles, N, K, out,
+                                   (hipStream_t)stream);
   return FERRET_ERR_SHAPE;
 }

@@ -97,8 +97,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-template <bool SILU, int WN, bool SPLIT, bool FULL>
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
 __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
+  static_assert(!SILU || GROUPED, "the SiLU epilogue is the grouped w13 GEMM's");
   using C = TileCfg<WN>;
   constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
   constexpr int TB_LD_PER_WAVE = C::kLdPerWave, TB_SA_OFF = C::kSaOff, TB_STAGE = C::kStage;
@@ -115,14 +116,15 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
   // ---- which tile.
   int e = 0, row0, nrows, nb;
-  if constexpr (SILU) {
-    // Grouped: bid = tile * n_blocks + nb.  Work-groups are dealt to the 8 XCDs
-    // round-robin by block id and n_blocks % 8 == 0, so every tile's block nb
-    // lands on XCD nb % 8: the row tiles of one expert share its weight block
-    // in that XCD's L2.
-    nb = blockIdx.x % p.n_blocks;
-    const int tile_idx = blockIdx.x / p.n_blocks;
-    if (tile_idx >= p.ntiles[0]) return;
+  if constexpr (GROUPED) {
+    // Grouped: bid = tile * nbp + nb, nbp = n_blocks rounded up to 8.  Work-
+    // groups are dealt to the 8 XCDs round-robin by block id, so every tile's
+    // block nb lands on XCD nb % 8: the row tiles of one expert share its
+    // weight block in that XCD's L2.  Padding blocks and tiles past ntiles exit.
+    const int nbp = (p.n_blocks + 7) & ~7;
+    nb = blockIdx.x % nbp;
+    const int tile_idx = blockIdx.x / nbp;
+    if (nb >= p.n_blocks || tile_idx >= p.ntiles[0]) return;
     e = p.tiles[3 * tile_idx];
     row0 = p.tiles[3 * tile_idx + 1];
     nrows = p.tiles[3 * tile_idx + 2];
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       const int row = (j - C::kWInstr) * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ swz_key(row);
       const int t = min(row, nrows - 1);
-      const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
+      const int tok = GROUPED ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
       goff[i] = (uint32_t)tok * (uint32_t)K + chunk * 16;
     }
   }
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   const float* sa_src = nullptr;
   if (sa_wave) {
     const int t = min((wave - (TB_WAVES - 2)) * 64 + lane, nrows - 1);
-    const int tok = SILU ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
+    const int tok = GROUPED ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
     sa_src = p.sa + (size_t)tok * nkb;
   }
   // Instruction i of this wave's share of stage `step` (i == TB_LD_PER_WAVE:
@@ -417,7 +419,9 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       for (int ni = 0; ni < 4; ++ni) *reinterpret_cast<f32x4*>(o + ni * 16 + 4 * g) = acc[ni][mi];
     } else {
       if (nb * TB_N + wn * 64 >= N) continue;  // wave's rows lie past N (N % 256 == 128)
-      uint16_t* o = p.out + (size_t)(row0 + tl) * N + nb * TB_N + wn * 64;
+      // dense: token row; grouped: the routed pair of the sorted row
+      const size_t orow = GROUPED ? (size_t)p.sorted_pair[row0 + tl] : (size_t)(row0 + tl);
+      uint16_t* o = p.out + orow * N + nb * TB_N + wn * 64;
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) {
         u32x2 v;
@@ -433,12 +437,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
-template <bool SILU, int WN, bool SPLIT, bool FULL>
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
 static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
   using C = TileCfg<WN>;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, WN, SPLIT, FULL>,
+  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
-  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, WN, SPLIT, FULL>), grid, dim3(C::kThreads), C::kLds, st, p);
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>), grid, dim3(C::kThreads), C::kLds, st, p);
   return (int)hipGetLastError();
 }
 
@@ -487,8 +491,8 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     p.partial = static_cast<float*>(ws);
     p.n_blocks = N / (64 * SPLITK_WN);
     const dim3 grid(p.n_blocks * p.m_blocks, used);
-    const int rc = M % TB_M == 0 ? launch_tiled<false, SPLITK_WN, true, true>(p, grid, st)
-                                 : launch_tiled<false, SPLITK_WN, true, false>(p, grid, st);
+    const int rc = M % TB_M == 0 ? launch_tiled<false, false, SPLITK_WN, true, true>(p, grid, st)
+                                 : launch_tiled<false, false, SPLITK_WN, true, false>(p, grid, st);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
@@ -498,8 +502,8 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
   // Dense tiles: with every token tile full (M % 128 == 0) the kernel skips
   // the per-wave count of occupied 16-token sub-tiles.
   p.n_blocks = (N + 255) / 256;
-  if (M % TB_M == 0) return launch_tiled<false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st);
-  return launch_tiled<false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st);
+  if (M % TB_M == 0) return launch_tiled<false, false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st);
+  return launch_tiled<false, false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st);
 }
 
 int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, const float* sw,
@@ -518,7 +522,32 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   p.N = N;
   p.K = K;
   p.n_blocks = (N / 2) / 128;
-  const int grid = max_tiles * p.n_blocks;
+  const long long grid = (long long)max_tiles * ((p.n_blocks + 7) & ~7);  // see the grouped tile mapping
   if (grid <= 0) return FERRET_OK;
-  return launch_tiled<true, 4, false, false>(p, dim3(grid), st);
+  if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
+  return launch_tiled<true, true, 4, false, false>(p, dim3((unsigned)grid), st);
+}
+
+// Prefill-sized MoE w2 / down projection: grouped tiles, bf16 store to the
+// routed pair's row; the A row of a sorted row is its pair too (topk = 1).
+int ferret_moe_w2_fp8_tiled(const void* h, const float* sh, const void* w, const float* sw,
+                            const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                            int max_tiles, int N, int K, void* out, hipStream_t st) {
+  TiledArgs p{};
+  p.a = static_cast<const uint8_t*>(h);
+  p.sa = sh;
+  p.b = static_cast<const uint8_t*>(w);
+  p.sb = sw;
+  p.out = static_cast<uint16_t*>(out);
+  p.sorted_pair = sorted_pair;
+  p.tiles = tiles;
+  p.ntiles = ntiles;
+  p.topk = 1;
+  p.N = N;
+  p.K = K;
+  p.n_blocks = (N + TileCfg<4>::kN - 1) / TileCfg<4>::kN;
+  const long long grid = (long long)max_tiles * ((p.n_blocks + 7) & ~7);
+  if (grid <= 0) return FERRET_OK;
+  if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
+  return launch_tiled<false, true, 4, false, false>(p, dim3((unsigned)grid), st);
 }

@@ -53,8 +53,10 @@ static int try_stream(const SkinnyArgs& a, int dense_tiles, int max_tiles, hipSt
   const long per = ((long)tiles * a.units_n + grid - 1) / grid;
   if (a.tiles && per / a.units_n + 2 > kStreamMaxTiles) return 1;
   // INT4 keeps at most one unit of scales ahead: ring depth <= KS.
+  constexpr int D2 = (F == kINT4 && D > 2) ? 2 : D;
   constexpr int D4 = (F == kINT4 && D > 4) ? 4 : D;
   switch (nkb / NW) {
+    case 2: return launch_stream<F, EPI, RB, NW, 2, D2>(a, dense_tiles, grid, st);
     case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, dense_tiles, grid, st);
     case 7: return launch_stream<F, EPI, RB, NW, 7, D>(a, dense_tiles, grid, st);
     case 8: return launch_stream<F, EPI, RB, NW, 8, D>(a, dense_tiles, grid, st);
@@ -178,6 +180,34 @@ int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, con
   const int rc = try_stream<kFP8, kSilu, STREAM_MOE_CFG>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kSilu, 2>(a, max_tiles, st);
+}
+
+// Decode-sized FP8 MoE w2 / down projection (tile_m = 16): the A row and the
+// output row of a sorted row are both its routed pair (topk = 1 indexing).
+int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, const float* sw,
+                             const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                             int max_tiles, int N, int K, void* out, hipStream_t st) {
+  SkinnyArgs a{};
+  a.w = static_cast<const uint8_t*>(w);
+  a.w_scale = sw;
+  a.x = static_cast<const uint8_t*>(h);
+  a.x_scale = sh;
+  a.out = static_cast<uint16_t*>(out);
+  a.sorted_pair = sorted_pair;
+  a.tiles = tiles;
+  a.ntiles = ntiles;
+  a.topk = 1;
+  a.N = N;
+  a.K = K;
+  if (max_tiles <= 0) return FERRET_OK;
+#ifndef STREAM_W2_CFG
+#define STREAM_W2_CFG 1, 6, 8
+#endif
+  constexpr int kCfg[] = {STREAM_W2_CFG};  // RB, D, NW
+  a.units_n = N / (16 * kCfg[0]);
+  const int rc = try_stream<kFP8, kStore, STREAM_W2_CFG>(a, 0, max_tiles, st);
+  if (rc != 1) return rc;
+  return launch_skinny<kFP8, kStore, 1>(a, max_tiles, st);
 }
 
 extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,

@@ -14,7 +14,7 @@ struct SkinnyArgs {
   const uint8_t* x;         // bf16 / e4m3 [T, K]
   const float* x_scale;     // FP8: f32 [T, K/128]
   const uint16_t* residual; // bf16 [M, N] or null (dense store only)
-  uint16_t* out;            // dense: bf16 [M, N]; SiLU: bf16 [P, N/2]
+  uint16_t* out;            // dense: bf16 [M, N]; grouped store: bf16 [P, N] (pair rows); SiLU: bf16 [P, N/2]
   const int32_t* sorted_pair;
   const int32_t* tiles;     // grouped: int32 [max_tiles, 3]; dense: null
   const int32_t* ntiles;
@@ -231,7 +231,9 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
     if constexpr (EPI == kStore) {
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[(w * RB + part) * kRedBlock + t * kRedStride + row];
-      const size_t o = (size_t)(row0 + t) * N + rowb[0] + part * 16 + row;
+      // dense: token row; grouped: the routed pair of the sorted row
+      const size_t orow = grouped ? (size_t)a.sorted_pair[row0 + t] : (size_t)(row0 + t);
+      const size_t o = orow * N + rowb[0] + part * 16 + row;
       if (a.residual) v += bf16_bits_to_f32(a.residual[o]);
       a.out[o] = f32_to_bf16_bits(v);
     } else {

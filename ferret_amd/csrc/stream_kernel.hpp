@@ -255,7 +255,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   u32x4 xv[KS][XV];
   float sx[KS];
   int cur_tile = -1;
-  int my_pair = 0;  // SiLU: routed pair of token column r (from sorted_pair)
+  int my_pair = 0;  // grouped: routed pair of token column r (from sorted_pair)
   int nrows = 0, row0 = 0;
 
   f32x4 acc[RB];
@@ -383,7 +383,10 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) v += rb_base[(w * RB + part) * kRedBlock + t * kRedStride + row];
-        if (t < nrows) a.out[(size_t)(row0 + t) * N + block_row(nu, part) + row] = f32_to_bf16_bits(v);
+        // dense: token row; grouped: the routed pair of column t (held by lane t;
+        // every wave runs this loop a uniform number of times)
+        const int orow = grouped ? __shfl(my_pair, t, 64) : row0 + t;
+        if (t < nrows) a.out[(size_t)orow * N + block_row(nu, part) + row] = f32_to_bf16_bits(v);
       }
     } else {
       const int idx = threadIdx.x;

@@ -31,6 +31,10 @@ SIGNATURES = {
                                     _c_int, _c_int, _vp, _vp]),
     "ferret_moe_w13_w4a16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _vp, _vp]),
+    "ferret_quant_act_e4m3": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
+    "ferret_moe_w2_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                   _c_int, _vp, _vp]),
+    "ferret_moe_combine": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "ferret_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
 }
 

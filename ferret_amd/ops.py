@@ -187,3 +187,50 @@ def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: 
         routing.tile_m, T, routing.topk, E, N, K, _dev(out, "out", torch.bfloat16, 2), _stream())
     _lib.check("ferret_moe_w13_w4a16", rc)
     return out
+
+
+def quant_act_e4m3(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tensor | None = None):
+    """bf16 x [M, K] -> (e4m3 q [M, K], fp32 scale [M, K/128]) by the 1x128 absmax/448 rule."""
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=FP8, device=x.device)
+    if scale is None:
+        scale = torch.empty((M, K // 128), dtype=torch.float32, device=x.device)
+    rc = _lib.load().ferret_quant_act_e4m3(_dev(x, "x", torch.bfloat16, 2), _dev(q, "q", (FP8, torch.uint8), 2),
+                                           _dev(scale, "scale", torch.float32, 2), M, K, _stream())
+    _lib.check("ferret_quant_act_e4m3", rc)
+    return q, scale
+
+
+def moe_w2_fp8(h: torch.Tensor, sh: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, routing: Routing,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[P, N] bf16 (pair order) = the FP8 block-scaled down projection of h [P, K] (pair order)."""
+    P, K = h.shape
+    E, N, K2 = w.shape
+    if K2 != K or E != routing.num_experts or P != routing.num_tokens * routing.topk:
+        raise ValueError("shape mismatch between h, w and routing")
+    if tuple(sh.shape) != (P, K // 128) or tuple(sw.shape) != (E, N // 128, K // 128):
+        raise ValueError("scale shapes must be sh [P, K/128], sw [E, N/128, K/128]")
+    if out is None:
+        out = torch.empty((P, N), dtype=torch.bfloat16, device=h.device)
+    rc = _lib.load().ferret_moe_w2_fp8(
+        _dev(h, "h", (FP8, torch.uint8), 2), _dev(sh, "sh", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
+        _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
+        routing.ntiles.data_ptr(), routing.max_tiles, routing.tile_m, P, E, N, K,
+        _dev(out, "out", torch.bfloat16, 2), _stream())
+    _lib.check("ferret_moe_w2_fp8", rc)
+    return out
+
+
+def moe_combine(o: torch.Tensor, weights: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[T, N] bf16 = sum_j weights[t, j] * o[t*topk + j] (fp32, j order)."""
+    T, topk = weights.shape
+    P, N = o.shape
+    if P != T * topk:
+        raise ValueError("o must hold T*topk rows in pair order")
+    if out is None:
+        out = torch.empty((T, N), dtype=torch.bfloat16, device=o.device)
+    rc = _lib.load().ferret_moe_combine(_dev(o, "o", torch.bfloat16, 2), _dev(weights, "weights", torch.float32, 2),
+                                        T, topk, N, _dev(out, "out", torch.bfloat16, 2), _stream())
+    _lib.check("ferret_moe_combine", rc)
+    return out

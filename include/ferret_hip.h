@@ -145,6 +145,46 @@ int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
                          int max_tiles, int tile_m, int T, int topk, int E, int N, int K,
                          void* out, void* stream);
 
+/*
+ * 1x128 activation quantizer: bf16 x [M,K] -> OCP e4m3 q [M,K] and fp32
+ * scale [M,K/128] with, per 128-element block of a row (fp32, correctly rounded
+ * division):  amax = max(|x| over the block, 1e-4);  q = e4m3_RNE(x * (448/amax));
+ * scale = amax / 448.  The input format of every FP8 entry point above.
+ * Replaces deep_gemm.per_token_cast_to_fp8 at its call site
+ * baselines/fp8-gemm/baseline_prefill.py:41 (layout of A / A_scale:
+ * tasks/fp8-group-gemm-dsv3-decode.yaml:19-20); DeepGEMM's own epsilon clamp is
+ * not vendored, the floor 1e-4 is this library's.  Requirements: M >= 1,
+ * K % 128 == 0.
+ */
+int ferret_quant_act_e4m3(const void* x, void* q, float* scale, int M, int K, void* stream);
+
+/*
+ * FP8 block-scaled MoE down projection (w2) grouped GEMM:
+ *   out[p, n] = sum_kb (sum_{k in kb} h[p,k] W[e][n,k]) * sh[p,kb] * sw[e][n/128,kb]
+ * for every routed pair p (expert e), h e4m3 [P,K] and sh f32 [P,K/128] in pair
+ * order (the w13 output quantized by ferret_quant_act_e4m3), w e4m3 [E,N,K],
+ * sw f32 [E,N/128,K/128], out bf16 [P,N] in pair order.  Tile inputs from
+ * ferret_moe_permute as for ferret_moe_w13_fp8.  Replaces the down GEMM
+ * (K = 2048 -> N = 7168) of tasks/fp8-group-gemm-dsv3-decode.yaml:11-13,67-86 and
+ * tasks/fp8-group-gemm-dsv3-prefill.yaml:15,76-95, run by grouped_fp8_gemm_bs
+ * (examples/fp8-group-gemm/v007_dsv3_decode_verified_105.cu:66-335).
+ * Requirements: N % 128 == 0, K % 128 == 0, K / 128 <= 128, tile_m 16 or 128.
+ */
+int ferret_moe_w2_fp8(const void* h, const float* sh, const void* w, const float* sw,
+                      const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                      int max_tiles, int tile_m, int P, int E, int N, int K, void* out, void* stream);
+
+/*
+ * Top-k weighted combine of the down-projection rows:
+ *   y[t, n] = bf16_RNE( sum_{j < topk} w[t, j] * o[t*topk + j, n] )
+ * o bf16 [T*topk, N] in pair order, w f32 [T, topk] (ferret_moe_route_topk's
+ * weights), y bf16 [T, N]; the fp32 sum runs in j order (deterministic).
+ * The reference has no combine kernel (its routing weights are computed and
+ * left unused by w13: baselines/kimi-moe-w13-int4/baseline_marlin.py:92-104,158);
+ * this is the build's own contract.  Requirements: N % 8 == 0, 1 <= topk <= 64.
+ */
+int ferret_moe_combine(const void* o, const float* w, int T, int topk, int N, void* y, void* stream);
+
 /* Workspace bytes an op can use (0 = none). op: 0 linear_bf16,
  * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
  * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts). */

@@ -16,12 +16,20 @@ float32, in the reference's summation form:
   ``correctness/compare_marlin_vs_ref.py:93-97``.
 * INT4 W4A16 MoE w13: ``fp32_oracle_w13_silu`` at
   ``correctness/compare_marlin_vs_ref.py:44-100``.
+* FP8 MoE w2 (down, K = 2048 -> N = 7168 at
+  ``tasks/fp8-group-gemm-dsv3-decode.yaml:11-13``): the block-scaled product of
+  ``cpu_ref_bs`` per routed pair, the pair's own activation row.
+* Top-k combine: sum_j w[t,j] * o[t*topk+j] in float32 (the build's own
+  contract; the reference's routing weights are left unused by w13,
+  ``baselines/kimi-moe-w13-int4/baseline_marlin.py:158``).
 
 Pinned by (tests/test_oracle_gemm.py): brute-force triple loops on tiny shapes,
 the all-scales-one reduction to a plain fp8 matmul, power-of-two scales (exact),
 single-K-block closed form, small-integer operands with exact sums, a planted
 transposition / dropped-block / wrong-expert mutant that each check rejects, and
-the SiLU closed form at known points.
+the SiLU closed form at known points; w2 against a per-pair brute-force loop
+and against fp8_blockscale_gemm on each expert's rows; the combine by one-hot
+weights (exact row selection) and power-of-two uniform weights (exact mean).
 """
 from __future__ import annotations
 
@@ -139,3 +147,38 @@ def moe_w13_w4a16(x_bits, wq, ws_bits, topk_ids, pairs=None, group: int = 32) ->
         for r, p in enumerate(plist):
             out[pos[p]] = res[r]
     return out
+
+
+def moe_w2_fp8(h_codes, sh, w_codes, sw, topk_ids, pairs=None) -> np.ndarray:
+    """FP8 block-scaled MoE down projection.
+
+    h_codes uint8 [P,K], sh float32 [P,K/128] (pair order: row p is pair p);
+    w_codes uint8 [E,N,K]; sw float32 [E,N/128,K/128]; topk_ids int [T,topk]
+    with T*topk = P.  out[p] = fp8_blockscale_gemm(h[p], W[expert(p)]).
+    Returns float32 [len(pairs), N] for the requested pairs, in the order given.
+    """
+    n = w_codes.shape[1]
+    pairs, groups = _pairs_by_expert(topk_ids, pairs)
+    out = np.zeros((pairs.size, n), dtype=np.float32)
+    pos = {int(p): i for i, p in enumerate(pairs)}
+    for e, plist in groups.items():
+        rows = np.array(plist)
+        res = fp8_blockscale_gemm(h_codes[rows], sh[rows], w_codes[e], sw[e])
+        for r, p in enumerate(plist):
+            out[pos[p]] = res[r]
+    return out
+
+
+def moe_combine(o_bits: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """y[t] = sum_j weights[t,j] * o[t*topk + j] in float32, j in order.
+
+    o_bits uint16 [T*topk, N] (bf16, pair order); weights float32 [T, topk].
+    Returns float32 [T, N] (not rounded).
+    """
+    w = _f32(weights)
+    t, topk = w.shape
+    o = bf16_bits_to_f32(o_bits).reshape(t, topk, -1)
+    y = np.zeros((t, o.shape[2]), dtype=np.float32)
+    for j in range(topk):
+        y = (y + w[:, j][:, None] * o[:, j, :]).astype(np.float32)
+    return y

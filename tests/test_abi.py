@@ -17,7 +17,8 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for must in ("launch_gemv", "ferret_linear_bf16", "ferret_fp8_gemm_blockscale", "ferret_moe_route_topk",
-                 "ferret_moe_permute", "ferret_moe_w13_fp8", "ferret_moe_w13_w4a16", "ferret_workspace_bytes"):
+                 "ferret_moe_permute", "ferret_moe_w13_fp8", "ferret_moe_w13_w4a16", "ferret_workspace_bytes",
+                 "ferret_quant_act_e4m3", "ferret_moe_w2_fp8", "ferret_moe_combine"):
         assert must in names
 
 
@@ -56,6 +57,15 @@ def test_argument_errors_are_returned_not_raised_without_gpu():
     assert L.ferret_workspace_bytes(4, 1024, 0, 0, 256) == 0          # one work-group
     assert L.ferret_workspace_bytes(4, 32768, 0, 0, 256) == 32 * 256 * 4
     assert L.ferret_moe_w13_w4a16(1, 1, 1, 1, 1, 1, 10, 128, 4, 8, 16, 64, 256, 1, None) == -2
+    assert L.ferret_quant_act_e4m3(None, 1, 1, 4, 256, None) == -1
+    assert L.ferret_quant_act_e4m3(1, 1, 1, 4, 200, None) == -2
+    assert L.ferret_quant_act_e4m3(1, 1, 1, 0, 256, None) == -2
+    assert L.ferret_moe_w2_fp8(1, 1, 1, 1, 1, 1, 1, 10, 16, 64, 8, 7168, 2048, None, None) == -1
+    assert L.ferret_moe_w2_fp8(1, 1, 1, 1, 1, 1, 1, 10, 16, 64, 8, 7100, 2048, 1, None) == -2
+    assert L.ferret_moe_w2_fp8(1, 1, 1, 1, 1, 1, 1, 10, 32, 64, 8, 7168, 2048, 1, None) == -2   # tile_m
+    assert L.ferret_moe_combine(1, 1, 4, 8, 100, 1, None) == -2
+    assert L.ferret_moe_combine(1, None, 4, 8, 128, 1, None) == -1
+    assert L.ferret_moe_combine(1, 1, 4, 0, 128, 1, None) == -2
 
 
 def test_python_ops_refuse_cpu_tensors():

@@ -185,3 +185,77 @@ def test_moe_w4a16_matches_explicit_dequant_matmul():
             g, u = gu[:N // 2], gu[N // 2:]
             ref = g / (1 + np.exp(-g)) * u
             assert np.allclose(out[t * topk + j], ref, rtol=1e-4, atol=1e-6)
+
+
+def test_moe_w2_brute_force_per_pair():
+    """Each output row is the block-scaled product of the pair's own h row with
+    its expert's W, checked by the float64 triple loop; a wrong-expert and a
+    token-indexed (p // topk) mutant are both rejected."""
+    rng = np.random.default_rng(21)
+    T, E, N, K, topk = 3, 4, 130, 256, 2
+    P = T * topk
+    h = _rand_fp8((P, K), rng)
+    sh = rng.uniform(0.5, 1.0, size=(P, K // 128)).astype(np.float32)
+    w = _rand_fp8((E, N, K), rng)
+    sw = rng.uniform(0.5, 1.0, size=(E, 2, K // 128)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:topk] for _ in range(T)]).astype(np.int32)
+    out = G.moe_w2_fp8(h, sh, w, sw, ids)
+    assert out.shape == (P, N)
+    for p in range(P):
+        e = ids.reshape(-1)[p]
+        ref = _brute_fp8(h[p:p + 1], sh[p:p + 1], w[e], sw[e])[0]
+        assert np.allclose(out[p], ref, rtol=1e-5, atol=1e-4 * np.abs(ref).max())
+    wrong = ids[:, ::-1].copy()
+    assert not np.allclose(G.moe_w2_fp8(h, sh, w, sw, wrong), out)
+    tok_rows = np.repeat(np.arange(T), topk)                      # mutant: h indexed by token
+    mut = G.moe_w2_fp8(h[tok_rows * topk], sh[tok_rows * topk], w, sw, ids)
+    assert not np.allclose(mut, out)
+
+
+def test_moe_w2_matches_dense_gemm_per_expert_and_subset():
+    rng = np.random.default_rng(22)
+    T, E, N, K, topk = 6, 3, 256, 384, 2
+    P = T * topk
+    h = _rand_fp8((P, K), rng)
+    sh = rng.uniform(0.1, 2.0, size=(P, K // 128)).astype(np.float32)
+    w = _rand_fp8((E, N, K), rng)
+    sw = rng.uniform(0.1, 2.0, size=(E, N // 128, K // 128)).astype(np.float32)
+    ids = rng.integers(0, E, size=(T, topk)).astype(np.int32)
+    out = G.moe_w2_fp8(h, sh, w, sw, ids)
+    flat = ids.reshape(-1)
+    for e in range(E):
+        rows = np.nonzero(flat == e)[0]
+        if rows.size:
+            ref = G.fp8_blockscale_gemm(h[rows], sh[rows], w[e], sw[e])
+            assert np.allclose(out[rows], ref, rtol=1e-6, atol=1e-6 * np.abs(ref).max())
+    sub = G.moe_w2_fp8(h, sh, w, sw, ids, pairs=np.array([5, 0, 11]))
+    # BLAS may sum a different row count in another order: equal to fp32 rounding
+    assert np.allclose(sub, out[[5, 0, 11]], rtol=1e-6, atol=1e-6 * np.abs(out).max())
+
+
+def test_moe_combine_one_hot_selects_rows_exactly():
+    rng = np.random.default_rng(23)
+    T, topk, N = 5, 4, 64
+    o = F.f32_to_bf16_bits(rng.standard_normal((T * topk, N)).astype(np.float32))
+    sel = rng.integers(0, topk, size=T)
+    wts = np.zeros((T, topk), np.float32)
+    wts[np.arange(T), sel] = 1.0
+    y = G.moe_combine(o, wts)
+    assert np.array_equal(y, F.bf16_bits_to_f32(o)[np.arange(T) * topk + sel])
+
+
+def test_moe_combine_power_of_two_mean_exact_and_order_mutant():
+    """Values in [1, 2) with 8-bit significands and weights 1/8: every partial
+    sum is exact in fp32, so y is the exact mean; summing a shifted row (a
+    wrong pair index) is rejected."""
+    rng = np.random.default_rng(24)
+    T, topk, N = 4, 8, 32
+    vals = (1.0 + rng.integers(0, 128, size=(T * topk, N)) / 128.0).astype(np.float32)
+    o = F.f32_to_bf16_bits(vals)
+    assert np.array_equal(F.bf16_bits_to_f32(o), vals)
+    wts = np.full((T, topk), 0.125, np.float32)
+    y = G.moe_combine(o, wts)
+    exact = vals.astype(np.float64).reshape(T, topk, N).mean(axis=1)
+    assert np.array_equal(y.astype(np.float64), exact)
+    shifted = np.roll(o, 1, axis=0)
+    assert not np.array_equal(G.moe_combine(shifted, wts), y)
