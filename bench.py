@@ -7,7 +7,8 @@ Default mode prints ONE JSON line for the driver:
 
 A step is one pass of the hot path over one batch of synthetic input that is
 already resident in HBM: the GEMM launch for the dense workloads; route +
-permute + w13 GEMM for the MoE workloads.  Weights of the dense workloads are
+permute + grouped GEMM (w13 or w2) for the MoE workloads; one quantizer or
+combine launch for those two workloads.  Weights of the dense workloads are
 rotated over enough copies (>= 512 MB) that no step finds its operands in the
 256 MB MALL.  `roofline` is measured live with HIP events on the launch stream
 around the dominant kernel; `cpu_baseline` times the CPU oracle on a bounded
@@ -46,7 +47,10 @@ FAMILIES = {
     "decode_linear": ["qwen3_gateup_M16"],
     "fp8_dense": ["dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"],
     "moe": ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill"],
+    "moe_down": ["dsv3_moe_w2_decode", "dsv3_moe_w2_prefill"],
 }
+DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
+MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = FAMILIES["decode_linear"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
 
 
@@ -67,22 +71,28 @@ class Runner:
         t0 = time.perf_counter()
         self.inp = W.make_inputs(wl, "cuda")
         self.copies = [self.inp]
-        if wl.kind in ("linear_bf16", "fp8_gemm"):
+        if wl.kind in DENSE_KINDS:
             wbytes = sum(t.numel() * t.element_size() for t in self.inp.values())
             ncopy = max(1, math.ceil(rotate_bytes / max(wbytes, 1)))
             self.copies += [{k: v.clone() for k, v in self.inp.items()} for _ in range(ncopy - 1)]
         self.ws = None
+        self.n_hit = 0
         if wl.kind in ("linear_bf16", "fp8_gemm"):
             shape = (wl.M, wl.N)
             self.outs = [torch.empty(shape, dtype=torch.bfloat16, device="cuda") for _ in self.copies]
-            self.n_hit = 0
             if wl.kind == "fp8_gemm" and ops.fp8_workspace_bytes(wl.M, wl.N, wl.K):
                 self.ws = torch.empty(ops.fp8_workspace_bytes(wl.M, wl.N, wl.K), dtype=torch.uint8, device="cuda")
+        elif wl.kind == "quant_act":
+            self.outs = [(torch.empty((wl.M, wl.K), dtype=torch.float8_e4m3fn, device="cuda"),
+                          torch.empty((wl.M, wl.K // 128), dtype=torch.float32, device="cuda")) for _ in self.copies]
+        elif wl.kind == "moe_combine":
+            self.outs = [torch.empty((wl.T, wl.N), dtype=torch.bfloat16, device="cuda") for _ in self.copies]
         else:
             self.ids, _ = ops.moe_route_topk(self.inp["logits"], wl.topk)
             self.rt = ops.moe_permute(self.ids, wl.E)
             self.n_hit = W.experts_hit(self.ids, wl.E)
-            self.outs = [torch.empty((wl.T * wl.topk, wl.N // 2), dtype=torch.bfloat16, device="cuda")]
+            cols = wl.N if wl.kind == "moe_fp8_w2" else wl.N // 2
+            self.outs = [torch.empty((wl.T * wl.topk, cols), dtype=torch.bfloat16, device="cuda")]
         torch.cuda.synchronize()
         self.bytes = W.algorithmic_bytes(wl, self.n_hit)
         self.flops = W.flops(wl)
@@ -100,13 +110,19 @@ class Runner:
             ops.fp8_gemm_blockscale(c["a"], c["sa"], c["b"], c["sb"], out=o, workspace=self.ws)
         elif wl.kind == "moe_fp8":
             ops.moe_w13_fp8(c["x"], c["sx"], c["w"], c["sw"], self.rt, out=o)
+        elif wl.kind == "moe_fp8_w2":
+            ops.moe_w2_fp8(c["h"], c["sh"], c["w"], c["sw"], self.rt, out=o)
+        elif wl.kind == "quant_act":
+            ops.quant_act_e4m3(c["x"], q=o[0], scale=o[1])
+        elif wl.kind == "moe_combine":
+            ops.moe_combine(c["o"], c["w"], out=o)
         else:
             ops.moe_w13_w4a16(c["x"], c["w"], c["ws"], self.rt, out=o)
 
     def step(self, i: int, ev=None):
         """One pass of the hot path; `ev` = (start, end) events bracket the GEMM."""
         wl, ops = self.wl, self.ops
-        if wl.kind in ("moe_fp8", "moe_w4a16"):
+        if wl.kind in MOE_KINDS:
             self.ids, _ = ops.moe_route_topk(self.inp["logits"], wl.topk, with_weights=False)
             self.rt = ops.moe_permute(self.ids, wl.E, self.rt.tile_m)
         if ev is not None:
@@ -127,7 +143,7 @@ def roofline_of(wl, runner, kernel_ms: float) -> dict:
     unit, bound = unit_of(wl)
     if bound == "mfma":
         achieved = runner.flops / (kernel_ms * 1e-3) / 1e12
-        peak = PEAK_FP8_TFLOPS if wl.kind in ("fp8_gemm", "moe_fp8") else PEAK_BF16_TFLOPS
+        peak = PEAK_FP8_TFLOPS if wl.kind in ("fp8_gemm", "moe_fp8", "moe_fp8_w2") else PEAK_BF16_TFLOPS
     else:
         achieved = runner.bytes / (kernel_ms * 1e-3) / 1e9
         peak = PEAK_HBM_GBPS
@@ -170,7 +186,7 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
     """
     import numpy as np
     import torch
-    from oracle import formats as F, gemm as G, metrics as MT, routing as R
+    from oracle import formats as F, gemm as G, metrics as MT, quant as Q, routing as R
 
     def bits16(t):
         return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
@@ -179,9 +195,31 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
         return t.contiguous().view(torch.uint8).cpu().numpy()
 
     inp, out = runner.inp, runner.output()
-    got_all = F.bf16_bits_to_f32(bits16(out))
+    got_all = None if wl.kind == "quant_act" else F.bf16_bits_to_f32(bits16(out))
     rng = np.random.default_rng(0)
-    if wl.kind == "linear_bf16":
+    check = None   # exact comparison (quantizer) instead of the GEMM error metric
+    if wl.kind == "quant_act":
+        nrows = min(wl.M, 2048)
+        rows = np.sort(rng.choice(wl.M, size=nrows, replace=False))
+        xs = F.bf16_bits_to_f32(bits16(inp["x"])[rows])
+        fn = lambda: Q.quant_act_1x128(xs)  # noqa: E731
+        s_flops = 2 * nrows * wl.K
+        s_bytes = nrows * wl.K * 3 + nrows * (wl.K // 128) * 4
+        sample = f"{nrows} of {wl.M} rows"
+        gq, gs = codes(out[0])[rows], out[1].cpu().numpy()[rows]
+        check = lambda r: bool(np.array_equal(gq, r[0]) and np.array_equal(gs, r[1]))  # noqa: E731
+        got = None
+    elif wl.kind == "moe_combine":
+        ntok = min(wl.T, 1024)
+        toks = np.sort(rng.choice(wl.T, size=ntok, replace=False))
+        prow = (toks[:, None] * wl.topk + np.arange(wl.topk)[None, :]).reshape(-1)
+        ob, wts = bits16(inp["o"])[prow], inp["w"].cpu().numpy()[toks]
+        fn = lambda: G.moe_combine(ob, wts)  # noqa: E731
+        s_flops = 2 * ntok * wl.topk * wl.N
+        s_bytes = ntok * wl.topk * (wl.N * 2 + 4) + ntok * wl.N * 2
+        sample = f"{ntok} of {wl.T} tokens x all {wl.N} columns"
+        got = got_all[toks]
+    elif wl.kind == "linear_bf16":
         xb, wb = bits16(inp["x"]), bits16(inp["w"])
         rows = np.arange(wl.M)
         fn = lambda: G.linear_bf16(xb, wb)  # noqa: E731
@@ -218,6 +256,11 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
             w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
             fn = lambda: G.moe_w13_fp8(x, sx, w, sw, sub, pairs=pairs)  # noqa: E731
             per_e = wl.N * wl.K
+        elif wl.kind == "moe_fp8_w2":
+            h, sh = codes(inp["h"]), inp["sh"].cpu().numpy()
+            w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
+            fn = lambda: G.moe_w2_fp8(h, sh, w, sw, sub, pairs=pairs)  # noqa: E731
+            per_e = wl.N * wl.K
         else:
             x = bits16(inp["x"])
             w, ws = inp["w"][ex_t].cpu().numpy(), bits16(inp["ws"][ex_t])
@@ -235,7 +278,11 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
         ref = fn()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    err, nbad = MT.fp8_rel_err(got, ref)
+    if check is not None:
+        ok = check(ref)
+        err, nbad = (0.0 if ok else float("inf")), 0
+    else:
+        err, nbad = MT.fp8_rel_err(got, ref)
     unit, bound = unit_of(wl)
     value = s_flops / med / 1e12 if bound == "mfma" else s_bytes / med / 1e9
     return {"value": round(value, 6), "unit": unit, "cores": _blas_threads(), "kind": "port",
@@ -314,7 +361,8 @@ def driver_mode(args) -> int:
 
 def dtype_of(wl) -> str:
     return {"linear_bf16": "bf16", "fp8_gemm": "e4m3 (fp32 accumulate)", "moe_fp8": "e4m3 (fp32 accumulate)",
-            "moe_w4a16": "int4 weights x bf16 (fp32 accumulate)"}[wl.kind]
+            "moe_w4a16": "int4 weights x bf16 (fp32 accumulate)", "moe_fp8_w2": "e4m3 (fp32 accumulate)",
+            "quant_act": "bf16 -> e4m3 (fp32 scale)", "moe_combine": "bf16 (fp32 accumulate)"}[wl.kind]
 
 
 def config_of(wl, runner) -> dict:
@@ -398,7 +446,9 @@ def main(argv=None) -> int:
         return 2
     if args.also is None:
         args.also = [k for k in ("dsv3_fp8_M16", "dsv3_fp8_M128", "qwen3_gateup_M16", "dsv3_moe_w13_decode",
-                                 "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill")] if args.workload == DEFAULT_WORKLOAD else []
+                                 "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill", "dsv3_moe_w2_decode",
+                                 "dsv3_moe_w2_prefill", "moe_quant_act_prefill", "moe_combine_prefill")
+                     ] if args.workload == DEFAULT_WORKLOAD else []
     import torch
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)

@@ -1,7 +1,9 @@
 """The benchmark configurations of the quantized-GEMM path and their seeded inputs.
 
-Seven workloads (the four math cases at their DeepSeek-V3 / Qwen3-8B / Kimi-K2
-shapes).  Inputs are generated with torch on any device from per-tensor seeds;
+Seven workloads for the four math cases at their DeepSeek-V3 / Qwen3-8B /
+Kimi-K2 shapes, plus the rest of the FP8 MoE layer: the w2 down projection
+(K = 2048 -> N = 7168, tasks/fp8-group-gemm-dsv3-decode.yaml:11-13), the 1x128
+activation quantizer in front of it and the top-k combine after it.  Inputs are generated with torch on any device from per-tensor seeds;
 the quantizer below is the build's absmax/448 rule (1x128 activation blocks,
 128x128 weight blocks, fp32 scales), the same rule DeepGEMM's
 per_token_cast_to_fp8 / per_block_cast_to_fp8 implement at the reference's call
@@ -23,7 +25,8 @@ FP8 = torch.float8_e4m3fn
 @dataclass(frozen=True)
 class Workload:
     key: str
-    kind: str            # "linear_bf16" | "fp8_gemm" | "moe_fp8" | "moe_w4a16"
+    kind: str            # "linear_bf16" | "fp8_gemm" | "moe_fp8" | "moe_w4a16" | "moe_fp8_w2"
+                         # | "quant_act" | "moe_combine"
     M: int = 0           # dense tokens
     N: int = 0           # output rows (per expert: gate + up)
     K: int = 0
@@ -55,6 +58,18 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
     Workload("dsv3_moe_w13_prefill", "moe_fp8", N=4096, K=7168, T=4096, E=256, topk=8, routing="zipf",
              zipf_s=1.1, bound="mfma", description="DSv3 FP8 MoE w13 prefill: 4096 tokens, Zipf(1.1) top-8 of 256",
              seeds={"logits": 9, "x": 10, "w": 100}),
+    Workload("dsv3_moe_w2_decode", "moe_fp8_w2", N=7168, K=2048, T=128, E=256, topk=8, routing="softmax",
+             description="DSv3 FP8 MoE w2 (down) decode: 1024 routed rows [P,2048] -> [P,7168], 256 experts",
+             seeds={"logits": 5, "x": 13, "w": 400}),
+    Workload("dsv3_moe_w2_prefill", "moe_fp8_w2", N=7168, K=2048, T=4096, E=256, topk=8, routing="zipf",
+             zipf_s=1.1, bound="mfma", description="DSv3 FP8 MoE w2 (down) prefill: 32768 routed rows, Zipf(1.1)",
+             seeds={"logits": 9, "x": 14, "w": 400}),
+    Workload("moe_quant_act_prefill", "quant_act", M=32768, K=2048,
+             description="1x128 e4m3 quantization of the w2 input at prefill: bf16 [32768,2048]",
+             seeds={"x": 15}),
+    Workload("moe_combine_prefill", "moe_combine", N=7168, T=4096, topk=8,
+             description="top-8 weighted combine at prefill: bf16 [32768,7168] -> [4096,7168]",
+             seeds={"x": 16, "logits": 17}),
 ]}
 
 
@@ -107,6 +122,12 @@ def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) ->
     others stay zero-filled); None generates all of them.
     """
     s = w.seeds
+    if w.kind == "quant_act":
+        return {"x": randn((w.M, w.K), s["x"], device).to(torch.bfloat16)}
+    if w.kind == "moe_combine":
+        o = randn((w.T * w.topk, w.N), s["x"], device).to(torch.bfloat16)
+        wts = torch.softmax(randn((w.T, w.topk), s["logits"], device), dim=1)
+        return {"o": o, "w": wts}
     if w.kind == "linear_bf16":
         x = randn((w.M, w.K), s["x"], device).to(torch.bfloat16)
         wt = randn((w.N, w.K), s["w"], device, std=0.02).to(torch.bfloat16)
@@ -127,6 +148,13 @@ def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) ->
         for e in ex:
             wq[e], sw[e] = quant_weight_128x128(randn((w.N, w.K), s["w"] + e, device))
         return {"logits": logits, "x": x, "sx": sx, "w": wq, "sw": sw}
+    if w.kind == "moe_fp8_w2":
+        h, sh = quant_act_1x128(randn((w.T * w.topk, w.K), s["x"], device))
+        wq = torch.zeros((w.E, w.N, w.K), dtype=FP8, device=device)
+        sw = torch.ones((w.E, w.N // 128, w.K // 128), dtype=torch.float32, device=device)
+        for e in ex:
+            wq[e], sw[e] = quant_weight_128x128(randn((w.N, w.K), s["w"] + e, device))
+        return {"logits": logits, "h": h, "sh": sh, "w": wq, "sw": sw}
     if w.kind == "moe_w4a16":
         x = randn((w.T, w.K), s["x"], device).to(torch.bfloat16)
         wq = torch.zeros((w.E, w.N, w.K // 8), dtype=torch.int32, device=device)
@@ -158,10 +186,21 @@ def algorithmic_bytes(w: Workload, n_experts_hit: int = 0) -> int:
     if w.kind == "moe_w4a16":
         per_e = w.N * w.K // 2 + w.N * (w.K // 32) * 2
         return n_experts_hit * per_e + w.T * w.K * 2 + P * (w.N // 2) * 2 + P * 4 * 2
+    if w.kind == "moe_fp8_w2":
+        per_e = w.N * w.K + (w.N // 128) * (w.K // 128) * 4
+        return n_experts_hit * per_e + P * w.K + P * (w.K // 128) * 4 + P * w.N * 2 + P * 4 * 2
+    if w.kind == "quant_act":
+        return w.M * w.K * 2 + w.M * w.K + w.M * (w.K // 128) * 4
+    if w.kind == "moe_combine":
+        return P * w.N * 2 + P * 4 + w.T * w.N * 2
     raise ValueError(w.kind)
 
 
 def flops(w: Workload) -> int:
     if w.kind in ("linear_bf16", "fp8_gemm"):
         return 2 * w.M * w.N * w.K
+    if w.kind == "quant_act":
+        return 2 * w.M * w.K               # one scale multiply + one |x| max per element
+    if w.kind == "moe_combine":
+        return 2 * w.T * w.topk * w.N
     return 2 * w.T * w.topk * w.N * w.K
