@@ -51,7 +51,7 @@ FAMILIES = {
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
-FAMILIES["all"] = FAMILIES["decode_linear"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
+FAMILIES["all"] = FAMILIES["decode_linear"] + FAMILIES["fp8_dense"] + FAMILIES["moe"] + FAMILIES["moe_down"]
 
 
 def log(*a):
