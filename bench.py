@@ -44,14 +44,16 @@ PEAK_FP8_TFLOPS = 5000.0
 PEAK_BF16_TFLOPS = 2500.0
 DEFAULT_WORKLOAD = "dsv3_fp8_M4096"
 FAMILIES = {
-    "decode_linear": ["qwen3_gateup_M16"],
+    "decode_linear": ["qwen3_qkv_M16", "qwen3_o_M16", "qwen3_gateup_M16", "qwen3_down_M16", "qwen3_lmhead_M16"],
+    "decode_linear_m1": ["qwen3_qkv_M1", "qwen3_o_M1", "qwen3_gateup_M1", "qwen3_down_M1", "qwen3_lmhead_M1"],
     "fp8_dense": ["dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"],
     "moe": ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill"],
     "moe_down": ["dsv3_moe_w2_decode", "dsv3_moe_w2_prefill"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
-FAMILIES["all"] = FAMILIES["decode_linear"] + FAMILIES["fp8_dense"] + FAMILIES["moe"] + FAMILIES["moe_down"]
+FAMILIES["all"] = (FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"]
+                   + FAMILIES["moe"] + FAMILIES["moe_down"])
 
 
 def log(*a):
@@ -105,7 +107,7 @@ class Runner:
         c = self.copies[i % len(self.copies)]
         o = self.outs[i % len(self.outs)]
         if wl.kind == "linear_bf16":
-            ops.linear_bf16(c["x"], c["w"], out=o)
+            ops.linear_bf16(c["x"], c["w"], residual=c.get("r"), out=o)
         elif wl.kind == "fp8_gemm":
             ops.fp8_gemm_blockscale(c["a"], c["sa"], c["b"], c["sb"], out=o, workspace=self.ws)
         elif wl.kind == "moe_fp8":
@@ -221,8 +223,9 @@ def cpu_baseline(wl, runner, budget_s: float = 15.0) -> dict:
         got = got_all[toks]
     elif wl.kind == "linear_bf16":
         xb, wb = bits16(inp["x"]), bits16(inp["w"])
+        rb = bits16(inp["r"]) if "r" in inp else None
         rows = np.arange(wl.M)
-        fn = lambda: G.linear_bf16(xb, wb)  # noqa: E731
+        fn = lambda: G.linear_bf16(xb, wb, rb)  # noqa: E731
         s_flops = 2 * wl.M * wl.N * wl.K
         s_bytes = runner.bytes
         sample = f"all {wl.M} rows x {wl.N} outputs"

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <atomic>
 #include <stdint.h>
 
 #include "../../include/ferret_hip.h"
@@ -148,6 +149,20 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     hipError_t _e = (expr);                    \
     if (_e != hipSuccess) return (int)_e;      \
   } while (0)
+
+// Raise a kernel's dynamic-LDS limit to `bytes` once per device (the call is a
+// host-side cost on every launch otherwise); devices past 64 set it each time.
+template <auto Kernel>
+inline hipError_t set_lds_limit_once(int bytes) {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 64;
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute((const void*)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_relaxed);
+  return e;
+}
 
 #define FERRET_REQUIRE(cond, code) \
   do {                             \

@@ -8,6 +8,7 @@ int ferret_fp8_gemm_skinny(const void* a, const float* sa, const void* b, const 
 int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
                           int N, int K, void* ws, size_t ws_bytes, hipStream_t st);
 size_t ferret_fp8_gemm_workspace(int M, int N, int K);
+size_t ferret_linear_bf16_workspace(int M, int N, int K);
 size_t ferret_moe_permute_workspace(long long num_pairs, int E);
 int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, const float* sw,
                               const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
@@ -38,6 +39,8 @@ extern "C" const char* ferret_error_string(int code) {
 
 extern "C" size_t ferret_workspace_bytes(int op, int M, int N, int K, int E) {
   (void)E;
+  if (op == 0 && M > 0 && N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0)
+    return ferret_linear_bf16_workspace(M, N, K);
   if (op == 1 && M > 16 && M > 0 && N > 0 && K >= 128) return ferret_fp8_gemm_workspace(M, N, K);
   if (op == 4 && M > 0 && E > 0) return ferret_moe_permute_workspace(M, E);
   return 0;

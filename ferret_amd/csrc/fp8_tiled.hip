@@ -440,8 +440,7 @@ using namespace ferret;
 template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
 static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
   using C = TileCfg<WN>;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
+  FERRET_HIP_CHECK((set_lds_limit_once<fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>>(C::kLds)));
   hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>), grid, dim3(C::kThreads), C::kLds, st, p);
   return (int)hipGetLastError();
 }

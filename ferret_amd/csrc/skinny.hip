@@ -43,8 +43,11 @@ static int cu_count() {
 // kernel), else the launch status.  KS = K-steps per wave = K / 128 / NW.
 template <int F, int EPI, int RB, int D, int NW = 8>
 static int try_stream(const SkinnyArgs& a, int dense_tiles, int max_tiles, hipStream_t st) {
-  const int nkb = a.K >> 7;
-  if (nkb % NW != 0) return 1;
+  // bf16 dense split-K: each work item covers K / nsplit (see stream_gemm_kernel)
+  const int nsplit = (F == kBF16 && a.tiles == nullptr && a.partial != nullptr) ? a.ksplit : 1;
+  if (nsplit < 1) return 1;
+  const int nkb = (a.K >> 7) / nsplit;
+  if ((a.K >> 7) % (NW * nsplit) != 0) return 1;
   // INT4 unit scales are copied as 16-byte chunks of the scale rows.
   if (F == kINT4 && ((reinterpret_cast<uintptr_t>(a.w_scale) & 15) != 0 || a.K % 256 != 0)) return 1;
   const int grid = cu_count();
@@ -99,17 +102,70 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
   return FERRET_ERR_SHAPE;
 }
 
+// y[m, n] = bf16(sum_{s < S} partial[s, m, n] (+ residual[m, n])), splits in order.
+__global__ __launch_bounds__(256) void linear_splitk_reduce_kernel(const float* __restrict__ partial, int S,
+                                                                   long long mn4, const uint16_t* __restrict__ res,
+                                                                   uint16_t* __restrict__ y) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < mn4; i += (long long)gridDim.x * 256) {
+    f32x4 v = reinterpret_cast<const f32x4*>(partial)[i];
+    for (int s = 1; s < S; ++s) {
+      const f32x4 p = reinterpret_cast<const f32x4*>(partial + (size_t)s * mn4 * 4)[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += p[j];
+    }
+    if (res) {
+      const u32x2 r = reinterpret_cast<const u32x2*>(res)[i];
+      v[0] += __uint_as_float(r[0] << 16);
+      v[1] += __uint_as_float(r[0] & 0xffff0000u);
+      v[2] += __uint_as_float(r[1] << 16);
+      v[3] += __uint_as_float(r[1] & 0xffff0000u);
+    }
+    reinterpret_cast<u32x2*>(y)[i] = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+}
+
+// K splits of the bf16 stream kernel for y = x.W^T: 1 when a work-group per CU
+// is already evenly loaded (>= 90 % of the 256 CUs' share), else the split with
+// the best balance whose K-steps per wave (of 8) the kernel instantiates.
+// Measured reason: 384 row units (QKV) leave half the CUs with one unit and
+// half with two; K = 12288 (Down) needs 12 K-steps per wave, more activation
+// registers than a wave has.
+static int linear_splits(int M, int N, int K) {
+  const int nkb = K / 128;
+  const long long units = (long long)((M + 15) / 16) * (N / 16);
+  const int ncu = cu_count();
+  auto ks_ok = [](int ks) { return ks == 2 || ks == 4 || ks == 7 || ks == 8; };
+  auto balance = [&](int s) {
+    const long long items = units * s;
+    const long long per = (items + ncu - 1) / ncu;
+    return (double)items / (double)(per * ncu);
+  };
+  if (nkb % 8 == 0 && ks_ok(nkb / 8) && balance(1) >= 0.9) return 1;
+  int best = 1;
+  double best_b = -1.0;
+  for (int s = 2; s <= 8; ++s) {
+    if (nkb % (8 * s) != 0 || !ks_ok(nkb / (8 * s))) continue;
+    const double b = balance(s);
+    if (b > best_b + 1e-9) { best = s; best_b = b; }
+  }
+  return best;
+}
+
 }  // namespace ferret
 
 using namespace ferret;
 
+size_t ferret_linear_bf16_workspace(int M, int N, int K) {
+  const int s = linear_splits(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
 extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* residual, void* y, int M,
                                   int N, int K, void* ws, size_t ws_bytes, void* stream) {
-  (void)ws;
-  (void)ws_bytes;
   FERRET_REQUIRE(x && w && y, FERRET_ERR_NULL);
   FERRET_REQUIRE(M >= 1 && N >= 16 && K >= 128, FERRET_ERR_SHAPE);
   FERRET_REQUIRE(N % 16 == 0 && K % 128 == 0 && K / 128 <= 128, FERRET_ERR_SHAPE);
+  const hipStream_t st = (hipStream_t)stream;
   SkinnyArgs a{};
   a.w = static_cast<const uint8_t*>(w);
   a.x = static_cast<const uint8_t*>(x);
@@ -119,14 +175,29 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   a.N = N;
   a.K = K;
   a.units_n = N / 16;
-  if (residual == nullptr) {
 #ifndef STREAM_BF16_CFG
 #define STREAM_BF16_CFG 1, 3, 8
 #endif
-    const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, (hipStream_t)stream);
-    if (rc != 1) return rc;
+  const int splits = linear_splits(M, N, K);
+  const size_t need = ferret_linear_bf16_workspace(M, N, K);
+  if (splits > 1 && ws != nullptr && ws_bytes >= need && (M * (long long)N) % 4 == 0) {
+    a.partial = static_cast<float*>(ws);
+    a.ksplit = splits;
+    const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
+    if (rc != 1) {
+      if (rc != 0) return rc;
+      const long long mn4 = (long long)M * N / 4;
+      const int grid = (int)std::min<long long>((mn4 + 255) / 256, 4096);
+      hipLaunchKernelGGL(linear_splitk_reduce_kernel, dim3(grid), dim3(256), 0, st, a.partial, splits, mn4,
+                         a.residual, a.out);
+      return (int)hipGetLastError();
+    }
+    a.partial = nullptr;
+    a.ksplit = 0;
   }
-  return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, (hipStream_t)stream);
+  const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
+  if (rc != 1) return rc;
+  return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, st);
 }
 
 extern "C" void launch_gemv(void* input, void* weight, void* residual, void* output, int N, int K,

@@ -23,6 +23,8 @@ struct SkinnyArgs {
   int N;                    // weight rows (per expert)
   int K;
   int units_n;              // row units per token tile
+  float* partial;           // stream kernel, bf16 dense split-K: fp32 [ksplit, M, N] (null: no split)
+  int ksplit;               // number of K splits when partial != null
 };
 
 template <int F>

@@ -141,7 +141,11 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 
   // ---- this work-group's units
   const int ntiles = grouped ? __builtin_amdgcn_readfirstlane(a.ntiles[0]) : dense_tiles;
-  const int units = ntiles * a.units_n;
+  // bf16 dense split-K: work item u = split * (ntiles * units_n) + unit; the
+  // item's waves cover K-steps [(split * NW + w) * KS, ... + KS).
+  const int nsplit = (F == kBF16 && !grouped && a.partial != nullptr) ? a.ksplit : 1;
+  const int units_per_split = ntiles * a.units_n;
+  const int units = units_per_split * nsplit;
   const int per = (units + gridDim.x - 1) / gridDim.x;
   const int u_begin = min(units, (int)blockIdx.x * per);
   const int u_end = min(units, u_begin + per);
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 
   // Grouped: copy this work-group's rows of the tile table to LDS once, so the
   // loop reads them without vector-memory loads (which would drain the ring).
-  const int t_first = u_begin / a.units_n;
+  const int t_first = (u_begin % units_per_split) / a.units_n;  // grouped: nsplit == 1
   if (grouped) {
     const int t_last = (u_end - 1) / a.units_n;
     for (int i = threadIdx.x; i < 3 * (t_last - t_first + 1); i += NW * 64) tinfo[i] = a.tiles[3 * t_first + i];
@@ -196,11 +200,13 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   const uint8_t* sc_src[SI > 0 ? SI : 1];
   bool sc_live[SI > 0 ? SI : 1];
   auto set_issue_unit = [&](int u) {
-    const int tile = u / a.units_n, nu = u % a.units_n;
+    const int su = u % units_per_split;
+    const int tile = su / a.units_n, nu = su % a.units_n;
+    const int kstep0 = ((u / units_per_split) * NW + wave) * KS;  // first K-step of this wave
     const int e = tile_expert(tile);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
-      ibase[rb] = a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)wave * KS * ROWB;
+      ibase[rb] = a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)kstep0 * ROWB;
     if constexpr (F == kINT4) {
 #pragma unroll
       for (int q = 0; q < SI; ++q) {
@@ -245,11 +251,6 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     }
   };
 
-  set_issue_unit(iu);
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < n_items) issue(d);
-
   // ---- activations of the current token tile (registers), per K-step of this wave
   constexpr int XV = (F == kFP8) ? 2 : 4;
   u32x4 xv[KS][XV];
@@ -257,45 +258,62 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   int cur_tile = -1;
   int my_pair = 0;  // grouped: routed pair of token column r (from sorted_pair)
   int nrows = 0, row0 = 0;
+  int cur_split = -1;
+  auto load_tile = [&](int u) {
+    const int split = u / units_per_split;
+    const int tile = (u % units_per_split) / a.units_n;
+    cur_tile = tile;
+    cur_split = split;
+    if (grouped) {
+      row0 = tinfo[3 * (tile - t_first) + 1];
+      nrows = tinfo[3 * (tile - t_first) + 2];
+    } else {
+      row0 = tile * 16;
+      nrows = min(16, a.M - row0);
+    }
+    const int tcol = min(r, nrows - 1);  // columns >= nrows compute garbage, never stored
+    int tok = row0 + tcol;
+    if (grouped) {
+      my_pair = a.sorted_pair[row0 + tcol];
+      tok = my_pair / a.topk;
+    }
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int ks = (split * NW + wave) * KS + k;
+      if constexpr (F == kFP8) {
+        const uint8_t* xp = a.x + (size_t)tok * K + (size_t)ks * 128 + 32 * g;
+        xv[k][0] = ld_u32x4(xp);
+        xv[k][1] = ld_u32x4(xp + 16);
+        sx[k] = a.x_scale[(size_t)tok * nkb + ks];
+      } else {
+        const uint8_t* xp = a.x + ((size_t)tok * K + (size_t)ks * 128 + 32 * g) * 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
+      }
+    }
+  };
+  // The first tile's activations go out before the ring prologue: issued first,
+  // they complete first, and the compiler's counted wait before their first use
+  // leaves the weight stream in flight.
+  load_tile(u_begin);
+
+  set_issue_unit(iu);
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < n_items) issue(d);
 
   f32x4 acc[RB];
   int buf = 0;
 
   for (int u = u_begin; u < u_end; ++u) {
-    const int tile = u / a.units_n;
+    const int split = u / units_per_split;
+    const int tile = (u % units_per_split) / a.units_n;
     const int nu = u % a.units_n;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (tile != cur_tile) {
-      cur_tile = tile;
-      if (grouped) {
-        row0 = tinfo[3 * (tile - t_first) + 1];
-        nrows = tinfo[3 * (tile - t_first) + 2];
-      } else {
-        row0 = tile * 16;
-        nrows = min(16, a.M - row0);
-      }
-      const int tcol = min(r, nrows - 1);  // columns >= nrows compute garbage, never stored
-      int tok = row0 + tcol;
-      if (grouped) {
-        my_pair = a.sorted_pair[row0 + tcol];
-        tok = my_pair / a.topk;
-      }
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int ks = wave * KS + k;
-        if constexpr (F == kFP8) {
-          const uint8_t* xp = a.x + (size_t)tok * K + (size_t)ks * 128 + 32 * g;
-          xv[k][0] = ld_u32x4(xp);
-          xv[k][1] = ld_u32x4(xp + 16);
-          sx[k] = a.x_scale[(size_t)tok * nkb + ks];
-        } else {
-          const uint8_t* xp = a.x + ((size_t)tok * K + (size_t)ks * 128 + 32 * g) * 2;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
-        }
-      }
-      wait_vmcnt<0>();  // once per token tile: drains the ring as well
+    if (tile != cur_tile || split != cur_split) {
+      load_tile(u);
+      wait_vmcnt<0>();  // a later token tile: drains the ring as well
     }
 
     const uint8_t* sb_unit = sclbuf + (u & 1) * C::kSclBuf;
@@ -386,7 +404,15 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
         // dense: token row; grouped: the routed pair of column t (held by lane t;
         // every wave runs this loop a uniform number of times)
         const int orow = grouped ? __shfl(my_pair, t, 64) : row0 + t;
-        if (t < nrows) a.out[(size_t)orow * N + block_row(nu, part) + row] = f32_to_bf16_bits(v);
+        const size_t o = (size_t)orow * N + block_row(nu, part) + row;
+        if (t < nrows) {
+          if (nsplit > 1) {
+            a.partial[(size_t)split * a.M * N + o] = v;  // summed (+ residual) by the reduce kernel
+          } else {
+            if (a.residual) v += bf16_bits_to_f32(a.residual[o]);
+            a.out[o] = f32_to_bf16_bits(v);
+          }
+        }
       }
     } else {
       const int idx = threadIdx.x;
@@ -410,8 +436,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 template <int F, int EPI, int RB, int NW, int KS, int D>
 static int launch_stream(const SkinnyArgs& a, int dense_tiles, int grid, hipStream_t st) {
   using C = StreamCfg<F, RB, NW, KS, D>;
-  FERRET_HIP_CHECK(hipFuncSetAttribute((const void*)stream_gemm_kernel<F, EPI, RB, NW, KS, D>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds));
+  FERRET_HIP_CHECK((set_lds_limit_once<stream_gemm_kernel<F, EPI, RB, NW, KS, D>>(C::kLds)));
   hipLaunchKernelGGL((stream_gemm_kernel<F, EPI, RB, NW, KS, D>), dim3(grid), dim3(NW * 64), C::kLds, st, a,
                      dense_tiles);
   return (int)hipGetLastError();

@@ -33,9 +33,19 @@ def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None) -> int:
     return t.data_ptr()
 
 
+def linear_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Split-K workspace ferret_linear_bf16 can use for this shape (0: none)."""
+    return int(_lib.load().ferret_workspace_bytes(0, M, N, K, 0))
+
+
 def linear_bf16(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor | None = None,
-                out: torch.Tensor | None = None) -> torch.Tensor:
-    """y[M,N] = x[M,K] @ w[N,K]^T (+ residual), bf16 in/out, fp32 accumulate."""
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M,N] = x[M,K] @ w[N,K]^T (+ residual), bf16 in/out, fp32 accumulate.
+
+    Shapes that split K (see ferret_hip.h) take their fp32 partials from
+    `workspace`, or from torch's caching allocator when none (or a too small
+    one) is passed.
+    """
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
@@ -47,8 +57,12 @@ def linear_bf16(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor | None 
         if tuple(residual.shape) != (M, N):
             raise ValueError("residual must be [M, N]")
         rp = _dev(residual, "residual", torch.bfloat16)
+    need = linear_workspace_bytes(M, N, K) if K % 128 == 0 and N % 16 == 0 else 0
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     rc = _lib.load().ferret_linear_bf16(_dev(x, "x", torch.bfloat16, 2), _dev(w, "w", torch.bfloat16, 2), rp,
-                                        _dev(out, "out", torch.bfloat16, 2), M, N, K, None, 0, _stream())
+                                        _dev(out, "out", torch.bfloat16, 2), M, N, K,
+                                        _dev(workspace, "workspace") if need else None, need, _stream())
     _lib.check("ferret_linear_bf16", rc)
     return out
 

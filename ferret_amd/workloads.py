@@ -36,6 +36,7 @@ class Workload:
     routing: str = ""    # "softmax" (N(0,1) logits) | "zipf"
     zipf_s: float = 0.0
     bound: str = "hbm"   # roofline that limits it on MI355X
+    residual: bool = False  # linear_bf16: y = x.W^T + residual
     description: str = ""
     seeds: dict = field(default_factory=dict)
 
@@ -44,6 +45,17 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
     Workload("qwen3_gateup_M16", "linear_bf16", M=16, N=24576, K=4096,
              description="Qwen3-8B decode GateUp: X bf16 [16,4096], W bf16 [24576,4096]",
              seeds={"x": 1, "w": 2}),
+    *[Workload(f"qwen3_{name.lower()}_M{m}", "linear_bf16", M=m, N=n, K=k, residual=res,
+               description=f"Qwen3-8B decode {name}: X bf16 [{m},{k}], W bf16 [{n},{k}]"
+                           + (" + residual" if res else ""),
+               seeds={"x": 1, "w": 20 + i, "r": 40 + i})
+      # tasks/qwen3-8b-decode-linear-bs16-b200.yaml:72-95 (M = 16) and
+      # tasks/qwen3-8b-decode-linear-b200.yaml:53-76 (M = 1)
+      for m in (16, 1)
+      for i, (name, n, k, res) in enumerate([("QKV", 6144, 4096, False), ("O", 4096, 4096, True),
+                                             ("GateUp", 24576, 4096, False), ("Down", 4096, 12288, True),
+                                             ("LMHead", 153600, 4096, False)])
+      if not (m == 16 and name == "GateUp")],
     Workload("dsv3_fp8_M16", "fp8_gemm", M=16, N=4096, K=7168,
              description="DeepSeek-V3 dense FP8 GEMM M=16", seeds={"a": 3, "b": 4}),
     Workload("dsv3_fp8_M128", "fp8_gemm", M=128, N=4096, K=7168,
@@ -131,6 +143,8 @@ def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) ->
     if w.kind == "linear_bf16":
         x = randn((w.M, w.K), s["x"], device).to(torch.bfloat16)
         wt = randn((w.N, w.K), s["w"], device, std=0.02).to(torch.bfloat16)
+        if w.residual:
+            return {"x": x, "w": wt, "r": randn((w.M, w.N), s["r"], device).to(torch.bfloat16)}
         return {"x": x, "w": wt}
     if w.kind == "fp8_gemm":
         a, sa = quant_act_1x128(randn((w.M, w.K), s["a"], device))
@@ -174,7 +188,7 @@ def experts_hit(ids: torch.Tensor, E: int) -> int:
 def algorithmic_bytes(w: Workload, n_experts_hit: int = 0) -> int:
     """Every operand byte read once + every output byte written once."""
     if w.kind == "linear_bf16":
-        return 2 * (w.N * w.K + w.M * w.K + w.M * w.N)
+        return 2 * (w.N * w.K + w.M * w.K + w.M * w.N * (2 if w.residual else 1))
     if w.kind == "fp8_gemm":
         return (w.M * w.K + w.M * (w.K // 128) * 4 + w.N * w.K + ((w.N + 127) // 128) * (w.K // 128) * 4
                 + w.M * w.N * 2)

@@ -55,7 +55,11 @@ void launch_gemv(void* input, void* weight, void* residual, void* output, int N,
  * of examples/qwen3-8b-decode-linear-bs16/v019_swapab_cg2_l2hints.cu:422-482
  * (kernel :138-391, split-K reduce :395-417).
  * Requirements: 1 <= M, N % 16 == 0, K % 128 == 0, K/128 <= 128.
- * `ws`/`ws_bytes` are accepted for ABI stability and may be NULL/0.
+ * `ws` (optional): with at least ferret_workspace_bytes(0, M, N, K, 0) bytes
+ * (non-zero when splitting K evens out the work over the CUs, e.g. N = 6144 or
+ * K = 12288 at M <= 16) the product runs split-K: fp32 partials in the
+ * workspace, summed in split order (+ residual) by a second kernel
+ * (deterministic); with NULL the same result comes unsplit.
  */
 int ferret_linear_bf16(const void* x, const void* w, const void* residual, void* y, int M, int N,
                        int K, void* ws, size_t ws_bytes, void* stream);
@@ -185,7 +189,7 @@ int ferret_moe_w2_fp8(const void* h, const float* sh, const void* w, const float
  */
 int ferret_moe_combine(const void* o, const float* w, int T, int topk, int N, void* y, void* stream);
 
-/* Workspace bytes an op can use (0 = none). op: 0 linear_bf16,
+/* Workspace bytes an op can use (0 = none). op: 0 linear_bf16 (split-K partials),
  * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
  * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts). */
 size_t ferret_workspace_bytes(int op, int M, int N, int K, int E);

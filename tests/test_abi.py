@@ -57,6 +57,9 @@ def test_argument_errors_are_returned_not_raised_without_gpu():
     assert L.ferret_workspace_bytes(4, 1024, 0, 0, 256) == 0          # one work-group
     assert L.ferret_workspace_bytes(4, 32768, 0, 0, 256) == 32 * 256 * 4
     assert L.ferret_moe_w13_w4a16(1, 1, 1, 1, 1, 1, 10, 128, 4, 8, 16, 64, 256, 1, None) == -2
+    assert L.ferret_workspace_bytes(0, 16, 6144, 4096, 0) == 2 * 16 * 6144 * 4    # QKV: 2 K splits
+    assert L.ferret_workspace_bytes(0, 16, 4096, 12288, 0) == 3 * 16 * 4096 * 4   # Down: 3 K splits
+    assert L.ferret_workspace_bytes(0, 16, 4096, 4096, 0) == 0                    # one unit per CU
     assert L.ferret_quant_act_e4m3(None, 1, 1, 4, 256, None) == -1
     assert L.ferret_quant_act_e4m3(1, 1, 1, 4, 200, None) == -2
     assert L.ferret_quant_act_e4m3(1, 1, 1, 0, 256, None) == -2

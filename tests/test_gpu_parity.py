@@ -60,6 +60,33 @@ def test_linear_bf16_small(ops, M, N, K, res):
     assert nbad == 0 and e < 5e-3
 
 
+@pytest.mark.parametrize("M,N,K,res", [(16, 6144, 4096, False), (16, 4096, 12288, True), (1, 4096, 12288, True),
+                                       (16, 4096, 4096, True), (5, 6144, 4096, True), (13, 4096, 12288, False)])
+def test_linear_bf16_split_k_and_residual_paths(hip, M, N, K, res):
+    """QKV- and Down-shaped products split K over a workspace (partials summed
+    in split order with the residual by a second kernel); O-shaped ones add the
+    residual in the stream kernel.  With the workspace, without it (same
+    product unsplit) and one byte short: all meet the oracle."""
+    _say(f"linear_bf16 split/residual M={M} N={N} K={K} res={res}")
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + N + K)
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    r = torch.randn((M, N), generator=g, device="cuda").to(torch.bfloat16) if res else None
+    ref = G.linear_bf16(bits16(x), bits16(w), bits16(r) if res else None)
+    need = int(hip.ferret_workspace_bytes(0, M, N, K, 0))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    for ws_ptr, ws_bytes, tag in ((ws.data_ptr(), need, "ws"), (None, 0, "null-ws"),
+                                  (ws.data_ptr(), max(need - 1, 0), "short-ws")):
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        rc = hip.ferret_linear_bf16(x.data_ptr(), w.data_ptr(), r.data_ptr() if res else None, y.data_ptr(),
+                                    M, N, K, ws_ptr, ws_bytes, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert rc == 0, tag
+        got = bf16_out(y)
+        e, nbad = MT.linear_rel_err(got, ref)
+        assert nbad == 0 and e < 5e-3, f"{tag}: {e}"
+
+
 def test_launch_gemv_compat(hip):
     """The reference ctypes ABI (M = 1) writes the same result as ferret_linear_bf16."""
     N, K = 256, 1024
