@@ -117,14 +117,16 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   // ---- which tile.
   int e = 0, row0, nrows, nb;
   if constexpr (GROUPED) {
-    // Grouped: bid = tile * nbp + nb, nbp = n_blocks rounded up to 8.  Work-
-    // groups are dealt to the 8 XCDs round-robin by block id, so every tile's
-    // block nb lands on XCD nb % 8: the row tiles of one expert share its
-    // weight block in that XCD's L2.  Padding blocks and tiles past ntiles exit.
-    const int nbp = (p.n_blocks + 7) & ~7;
-    nb = blockIdx.x % nbp;
-    const int tile_idx = blockIdx.x / nbp;
-    if (nb >= p.n_blocks || tile_idx >= p.ntiles[0]) return;
+    // Grouped: bid = tile * n_blocks + nb.  Work-groups are dealt to the 8
+    // XCDs round-robin by block id: with n_blocks a multiple of 8, block nb of
+    // every tile lands on XCD nb % 8 and the row tiles of one expert share its
+    // weight block in that XCD's L2; otherwise the assignment rotates from
+    // tile to tile, which keeps the XCDs evenly loaded (padding each tile to a
+    // multiple of 8 blocks left the XCDs of the padding a quarter idle at
+    // n_blocks = 28).  Tiles past ntiles exit.
+    nb = blockIdx.x % p.n_blocks;
+    const int tile_idx = blockIdx.x / p.n_blocks;
+    if (tile_idx >= p.ntiles[0]) return;
     e = p.tiles[3 * tile_idx];
     row0 = p.tiles[3 * tile_idx + 1];
     nrows = p.tiles[3 * tile_idx + 2];
@@ -521,7 +523,7 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   p.N = N;
   p.K = K;
   p.n_blocks = (N / 2) / 128;
-  const long long grid = (long long)max_tiles * ((p.n_blocks + 7) & ~7);  // see the grouped tile mapping
+  const long long grid = (long long)max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
   if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
   return launch_tiled<true, true, 4, false, false>(p, dim3((unsigned)grid), st);
@@ -545,7 +547,7 @@ int ferret_moe_w2_fp8_tiled(const void* h, const float* sh, const void* w, const
   p.N = N;
   p.K = K;
   p.n_blocks = (N + TileCfg<4>::kN - 1) / TileCfg<4>::kN;
-  const long long grid = (long long)max_tiles * ((p.n_blocks + 7) & ~7);
+  const long long grid = (long long)max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
   if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
   return launch_tiled<false, true, 4, false, false>(p, dim3((unsigned)grid), st);

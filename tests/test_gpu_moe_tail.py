@@ -114,7 +114,7 @@ def test_moe_w2_fp8_small(ops, T, E, N, K, topk, tile_m):
 
 
 def test_moe_w2_fp8_padded_grid_and_empty_experts(ops):
-    """N = 7168 has 28 row blocks per tile (the grid pads to 32); two of the
+    """N = 7168 has 28 row blocks per tile (not a multiple of the 8 XCDs); two of the
     eight experts receive no pair."""
     _say("moe_w2_fp8 padded grid")
     T, E, N, K, topk = 96, 8, 7168, 2048, 2
