@@ -308,6 +308,37 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       wbf[ni][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
       wbf[ni][3] = e4m3x8_to_bf16x8(hi[2], hi[3]);
     }
+    // Keep the widening in X: unpinned, the compiler sinks most of the cvts
+    // past the copy branches into Y, where they queue behind the same wave's
+    // MFMAs instead of overlapping the partner wave's (8 % of the M = 4096
+    // GEMM; the 4-wave tiles are faster unpinned).
+    if constexpr (WN == 4) {
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(abf[mi][j]));
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(wbf[ni][j]));
+    }
+  };
+  // Issue priority of the wave (s_setprio; the arbiter otherwise favours the
+  // older waves, token half 0).  Y (MFMA) phases run above X phases, and
+  // token half 1 above half 0 in either, so half 0 no longer races ahead and
+  // idles at the barrier while half 1 widens its fragments alone.
+  auto set_prio = [&](bool y) {
+    if constexpr (WN == 4) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (y) {
+        if (wm == 1) __builtin_amdgcn_s_setprio(3);
+        else __builtin_amdgcn_s_setprio(2);
+      } else {
+        if (wm == 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   // Phase Y with this wave's share of the copy of stage `istep` (istep < 0:
   // none) spread over its MFMA blocks: instruction i goes after block 2i+1
@@ -317,6 +348,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   auto phase_y_copy = [&](auto mic, int istep) {
     constexpr int MI = decltype(mic)::value;
     constexpr int NB = 4 * MI;
+    set_prio(true);
     if constexpr (NB == 0) {
       if (istep >= 0) {
 #pragma unroll
@@ -345,6 +377,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
         }
       }
     }
+    set_prio(false);
   };
   auto barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
