@@ -49,11 +49,16 @@ FAMILIES = {
     "fp8_dense": ["dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"],
     "moe": ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill"],
     "moe_down": ["dsv3_moe_w2_decode", "dsv3_moe_w2_prefill"],
+    "fp8_attn_tp8": [f"dsv3_{p}_M{m}" for m in (1, 16) for p in ("q_b_proj", "kv_b_proj", "o_proj")]
+                    + ["dsv3_q_b_proj_M512", "dsv3_o_proj_M512"],
+    "fp8_attn_prefill_tp8": [f"dsv3_{p}_M{m}" for m in (512, 1024, 2048, 4096, 8192)
+                             for p in ("q_b_proj", "kv_b_proj", "o_proj")],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
-FAMILIES["all"] = (FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"]
-                   + FAMILIES["moe"] + FAMILIES["moe_down"])
+FAMILIES["all"] = list(dict.fromkeys(
+    FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
+    + FAMILIES["moe_down"] + FAMILIES["fp8_attn_tp8"] + FAMILIES["fp8_attn_prefill_tp8"]))
 
 
 def log(*a):

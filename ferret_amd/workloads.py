@@ -1,9 +1,11 @@
 """The benchmark configurations of the quantized-GEMM path and their seeded inputs.
 
-Seven workloads for the four math cases at their DeepSeek-V3 / Qwen3-8B /
-Kimi-K2 shapes, plus the rest of the FP8 MoE layer: the w2 down projection
-(K = 2048 -> N = 7168, tasks/fp8-group-gemm-dsv3-decode.yaml:11-13), the 1x128
-activation quantizer in front of it and the top-k combine after it.  Inputs are generated with torch on any device from per-tensor seeds;
+The four math cases at their DeepSeek-V3 / Qwen3-8B / Kimi-K2 shapes (the
+Qwen3-8B decode projections at M = 1 and 16, the DeepSeek-V3 TP8 attention
+projections from M = 1 to 8192), plus the rest of the FP8 MoE layer: the w2
+down projection (K = 2048 -> N = 7168, tasks/fp8-group-gemm-dsv3-decode.yaml:11-13),
+the 1x128 activation quantizer in front of it and the top-k combine after it.
+Inputs are generated with torch on any device from per-tensor seeds;
 the quantizer below is the build's absmax/448 rule (1x128 activation blocks,
 128x128 weight blocks, fp32 scales), the same rule DeepGEMM's
 per_token_cast_to_fp8 / per_block_cast_to_fp8 implement at the reference's call
@@ -62,6 +64,15 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
              description="DeepSeek-V3 dense FP8 GEMM M=128", seeds={"a": 3, "b": 4}),
     Workload("dsv3_fp8_M4096", "fp8_gemm", M=4096, N=4096, K=7168, bound="mfma",
              description="DeepSeek-V3 dense FP8 GEMM M=4096", seeds={"a": 3, "b": 4}),
+    # DeepSeek-V3 attention projections at TP = 8 (per-rank shapes): decode and
+    # a 512-token chunk (tasks/fp8-gemm-dense-tp8.yaml:36-74) and prefill with
+    # M up to the 8K kv_len of kv_b_proj (tasks/fp8-gemm-prefill-tp8.yaml:44-117).
+    *[Workload(f"dsv3_{proj}_M{m}", "fp8_gemm", M=m, N=n, K=k, bound="mfma" if m >= 512 else "hbm",
+               description=f"DeepSeek-V3 TP8 {proj} FP8 GEMM: A e4m3 [{m},{k}], B e4m3 [{n},{k}]",
+               seeds={"a": 30 + i, "b": 34 + i})
+      for m in (1, 16, 512, 1024, 2048, 4096, 8192)
+      for i, (proj, k, n) in enumerate([("q_b_proj", 1536, 3072), ("kv_b_proj", 512, 4096),
+                                        ("o_proj", 2048, 7168)])],
     Workload("dsv3_moe_w13_decode", "moe_fp8", N=4096, K=7168, T=128, E=256, topk=8, routing="softmax",
              description="DSv3 FP8 MoE w13 decode: 128 tokens, top-8 of 256", seeds={"logits": 5, "x": 6, "w": 100}),
     Workload("kimi_w4a16_w13_decode", "moe_w4a16", N=4096, K=7168, T=64, E=384, topk=8, routing="softmax",

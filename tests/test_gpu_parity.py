@@ -333,7 +333,12 @@ def test_int4_dequant_bit_exact_via_one_hot_activation(ops):
 
 # ------------------------------------------------------------------ full sizes
 
-@pytest.mark.parametrize("key", ["qwen3_gateup_M16", "dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"])
+_ATTN_TP8 = [f"dsv3_{p}_M{m}" for m in (1, 16, 512, 1024, 2048, 4096, 8192)
+             for p in ("q_b_proj", "kv_b_proj", "o_proj")]
+
+
+@pytest.mark.parametrize("key", ["qwen3_gateup_M16", "dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"]
+                         + _ATTN_TP8)
 def test_dense_full_size(ops, key):
     from ferret_amd import workloads as W
     wl = W.WORKLOADS[key]
