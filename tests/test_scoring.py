@@ -112,6 +112,23 @@ def test_mi355x_task_files_load_and_match_bench_families():
     assert set(by_name) == set(bench.FAMILIES["all"])
 
 
+def test_task_config_args_match_the_workloads_they_name():
+    """Every task config names a workload whose shape is the config's args, and
+    every family member is a workload."""
+    import bench
+    from ferret_amd import workloads as W
+    for fam, keys in bench.FAMILIES.items():
+        assert all(k in W.WORKLOADS for k in keys), fam
+    for f in sorted(os.listdir(TASKS)):
+        for c in S.load_task_spec(os.path.join(TASKS, f)).configs:
+            wl = W.WORKLOADS[c.name]
+            for arg, val in c.args.items():
+                if arg == "zipf_s":
+                    assert wl.zipf_s == val, (c.name, arg)
+                else:
+                    assert getattr(wl, arg) == val, (c.name, arg, getattr(wl, arg), val)
+
+
 def test_bench_lines_score_through_the_parser():
     out = ('[log] noise\nKERNEL_RESULT {"x": 10.0, "y": 0.0}\n'
            'KERNEL_RESULT_REFERENCE {"x": 0.5, "y": 0.25}\nROOFLINE {"x": {"frac": 0.8}}\n')
