@@ -433,11 +433,45 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   }
 
   // ---- epilogue. acc[ni][mi][i]: weight row wfrag_row[ni] - r + 4g + i, token column r.
+  if constexpr (!SILU && !SPLIT) {
+    // bf16 store.  Every wave has passed the last barrier (all X phases and
+    // stage copies are done), so the ring is idle: the wave stages its 64 x 64
+    // sub-tile through its own LDS rows (pitch 144 B: the 16 rows of one
+    // write land on distinct banks) and stores whole 128-B row segments, 16 B
+    // per lane.  Direct 8-B stores (16 rows x 32 B per instruction) took
+    // ~2 us per work-group; staged, the short-K GEMMs run 10-15 % faster.
+    if (nb * TB_N + wn * 64 >= N) return;  // wave's rows lie past N (N % 256 == 128)
+    constexpr int PITCH = 144;
+    uint8_t* stg = lds + wave * 64 * PITCH;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    const int tl = wm * 64 + mi * 16 + r;  // token row inside the tile
-    if (tl >= nrows) continue;
-    if constexpr (SILU) {
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        u32x2 v;
+        v[0] = pack_bf16x2(acc[ni][mi][0], acc[ni][mi][1]);
+        v[1] = pack_bf16x2(acc[ni][mi][2], acc[ni][mi][3]);
+        *reinterpret_cast<u32x2*>(stg + (mi * 16 + r) * PITCH + ni * 32 + g * 8) = v;
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own rows are written
+    const int chunk = lane & 7;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int rw = it * 8 + (lane >> 3);
+      const int tl = wm * 64 + rw;  // token row inside the tile
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rw * PITCH + chunk * 16);
+      if (tl < nrows) {
+        // dense: token row; grouped: the routed pair of the sorted row
+        const size_t orow = GROUPED ? (size_t)p.sorted_pair[row0 + tl] : (size_t)(row0 + tl);
+        *reinterpret_cast<u32x4*>(p.out + orow * N + nb * TB_N + wn * 64 + chunk * 8) = v;
+      }
+    }
+  } else if constexpr (SILU) {
+    // silu(gate) * up, bf16, to the routed pair's row (staging these 64-B
+    // rows through the LDS measured no faster).
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int tl = wm * 64 + mi * 16 + r;  // token row inside the tile
+      if (tl >= nrows) continue;
       const int pair = p.sorted_pair[row0 + tl];
       uint16_t* o = p.out + (size_t)pair * (N / 2) + nb * (TB_N / 2) + wn * 32;
 #pragma unroll
@@ -447,23 +481,16 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
         v[1] = pack_bf16x2(silu_mul(acc[ni][mi][2], acc[ni + 2][mi][2]), silu_mul(acc[ni][mi][3], acc[ni + 2][mi][3]));
         *reinterpret_cast<u32x2*>(o + ni * 16 + 4 * g) = v;
       }
-    } else if constexpr (SPLIT) {
-      if (nb * TB_N + wn * 64 >= N) continue;
+    }
+  } else {
+    // split-K: fp32 partials, 16 B per lane.
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int tl = wm * 64 + mi * 16 + r;  // token row inside the tile
+      if (tl >= nrows || nb * TB_N + wn * 64 >= N) continue;
       float* o = p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64;
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) *reinterpret_cast<f32x4*>(o + ni * 16 + 4 * g) = acc[ni][mi];
-    } else {
-      if (nb * TB_N + wn * 64 >= N) continue;  // wave's rows lie past N (N % 256 == 128)
-      // dense: token row; grouped: the routed pair of the sorted row
-      const size_t orow = GROUPED ? (size_t)p.sorted_pair[row0 + tl] : (size_t)(row0 + tl);
-      uint16_t* o = p.out + orow * N + nb * TB_N + wn * 64;
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) {
-        u32x2 v;
-        v[0] = pack_bf16x2(acc[ni][mi][0], acc[ni][mi][1]);
-        v[1] = pack_bf16x2(acc[ni][mi][2], acc[ni][mi][3]);
-        *reinterpret_cast<u32x2*>(o + ni * 16 + 4 * g) = v;
-      }
     }
   }
 }
