@@ -53,6 +53,8 @@ FAMILIES = {
                     + ["dsv3_q_b_proj_M512", "dsv3_o_proj_M512"],
     "fp8_attn_prefill_tp8": [f"dsv3_{p}_M{m}" for m in (512, 1024, 2048, 4096, 8192)
                              for p in ("q_b_proj", "kv_b_proj", "o_proj")],
+    "fp8_attn_prefill_large_m": ["dsv3_o_proj_M2048", "dsv3_q_b_proj_M8192", "dsv3_kv_b_proj_M8192",
+                                 "dsv3_o_proj_M4096", "dsv3_o_proj_M8192"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
