@@ -55,12 +55,16 @@ FAMILIES = {
                              for p in ("q_b_proj", "kv_b_proj", "o_proj")],
     "fp8_attn_prefill_large_m": ["dsv3_o_proj_M2048", "dsv3_q_b_proj_M8192", "dsv3_kv_b_proj_M8192",
                                  "dsv3_o_proj_M4096", "dsv3_o_proj_M8192"],
+    "moe_ep8_decode": [f"dsv3_ep8_{p}_M{m}" for m in (1, 4, 8, 16) for p in ("gate_up", "down")],
+    "moe_ep8_prefill": [f"dsv3_ep8_{p}_M{m}" for m in (64, 128, 256, 512) for p in ("gate_up", "down")],
+    "kimi_tp8": ["kimi_w4a16_w13_T8_tp8"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(
     FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
-    + FAMILIES["moe_down"] + FAMILIES["fp8_attn_tp8"] + FAMILIES["fp8_attn_prefill_tp8"]))
+    + FAMILIES["moe_down"] + FAMILIES["fp8_attn_tp8"] + FAMILIES["fp8_attn_prefill_tp8"]
+    + FAMILIES["moe_ep8_decode"] + FAMILIES["moe_ep8_prefill"] + FAMILIES["kimi_tp8"]))
 
 
 def log(*a):

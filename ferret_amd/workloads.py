@@ -35,7 +35,7 @@ class Workload:
     T: int = 0           # MoE tokens
     E: int = 0
     topk: int = 0
-    routing: str = ""    # "softmax" (N(0,1) logits) | "zipf"
+    routing: str = ""    # "softmax" (N(0,1) logits) | "zipf" | "uniform" (T/E rows per expert)
     zipf_s: float = 0.0
     bound: str = "hbm"   # roofline that limits it on MI355X
     residual: bool = False  # linear_bf16: y = x.W^T + residual
@@ -73,6 +73,21 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
       for m in (1, 16, 512, 1024, 2048, 4096, 8192)
       for i, (proj, k, n) in enumerate([("q_b_proj", 1536, 3072), ("kv_b_proj", 512, 4096),
                                         ("o_proj", 2048, 7168)])],
+    # The reference's own per-rank MoE tasks (EP 8: 32 local experts, uniform
+    # segments of M rows per expert, its m_indices = arange(M_total) // M
+    # stand-in): tasks/fp8-group-gemm-dsv3-decode.yaml:31-86 and
+    # tasks/fp8-group-gemm-dsv3-prefill.yaml:40-95.
+    *[Workload(f"dsv3_ep8_{proj}_M{m}", kind, N=n, K=k, T=32 * m, E=32, topk=1, routing="uniform",
+               bound="mfma" if m >= 64 else "hbm",
+               description=f"DSv3 FP8 grouped GEMM, EP8 rank: 32 experts x {m} rows, {proj} K={k} -> N={n}",
+               seeds={"logits": 0, "x": 60 + i, "w": 700 + 100 * i})
+      for m in (1, 4, 8, 16, 64, 128, 256, 512)
+      for i, (proj, kind, k, n) in enumerate([("gate_up", "moe_fp8", 7168, 4096),
+                                             ("down", "moe_fp8_w2", 2048, 7168)])],
+    # tasks/kimi-moe-w13-int4-grouped-gemm.yaml:35-40 (TP 8 rank: N_r = 2 I_r = 512)
+    Workload("kimi_w4a16_w13_T8_tp8", "moe_w4a16", N=512, K=7168, T=8, E=384, topk=8, routing="softmax",
+             description="Kimi-K2 INT4 W4A16 MoE w13, TP8 rank: 8 tokens, top-8 of 384, N_r=512",
+             seeds={"logits": 18, "x": 19, "w": 900}),
     Workload("dsv3_moe_w13_decode", "moe_fp8", N=4096, K=7168, T=128, E=256, topk=8, routing="softmax",
              description="DSv3 FP8 MoE w13 decode: 128 tokens, top-8 of 256", seeds={"logits": 5, "x": 6, "w": 100}),
     Workload("kimi_w4a16_w13_decode", "moe_w4a16", N=4096, K=7168, T=64, E=384, topk=8, routing="softmax",
@@ -163,6 +178,10 @@ def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) ->
         return {"a": a, "sa": sa, "b": b, "sb": sb}
     if w.routing == "zipf":
         logits = zipf_logits(w.T, w.E, w.zipf_s, s["logits"], device)
+    elif w.routing == "uniform":
+        # top-1 of a one-hot row: token t goes to expert t // (T / E)
+        logits = torch.zeros((w.T, w.E), dtype=torch.float32, device=device)
+        logits[torch.arange(w.T, device=device), torch.arange(w.T, device=device) // (w.T // w.E)] = 1.0
     else:
         logits = randn((w.T, w.E), s["logits"], device)
     ex = range(w.E) if experts is None else experts

@@ -361,7 +361,9 @@ def test_dense_full_size(ops, key):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "non-deterministic output"
 
 
-@pytest.mark.parametrize("key", ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill"])
+@pytest.mark.parametrize("key", ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill",
+                                 "kimi_w4a16_w13_T8_tp8"]
+                         + [f"dsv3_ep8_{p}_M{m}" for m in (1, 16, 64, 512) for p in ("gate_up", "down")])
 def test_moe_full_size(ops, key):
     from ferret_amd import workloads as W
     wl = W.WORKLOADS[key]
@@ -379,6 +381,9 @@ def test_moe_full_size(ops, key):
     if wl.kind == "moe_fp8":
         out = ops.moe_w13_fp8(inp["x"], inp["sx"], inp["w"], inp["sw"], rt)
         out2 = ops.moe_w13_fp8(inp["x"], inp["sx"], inp["w"], inp["sw"], rt)
+    elif wl.kind == "moe_fp8_w2":
+        out = ops.moe_w2_fp8(inp["h"], inp["sh"], inp["w"], inp["sw"], rt)
+        out2 = ops.moe_w2_fp8(inp["h"], inp["sh"], inp["w"], inp["sw"], rt)
     else:
         out = ops.moe_w13_w4a16(inp["x"], inp["w"], inp["ws"], rt)
         out2 = ops.moe_w13_w4a16(inp["x"], inp["w"], inp["ws"], rt)
@@ -386,7 +391,7 @@ def test_moe_full_size(ops, key):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "non-deterministic output"
     pairs, experts = moe_sample_pairs(ids_np, wl.E)
     # Host copies of only the sampled experts' weights.
-    x_host = codes8(inp["x"]) if wl.kind == "moe_fp8" else bits16(inp["x"])
+    x_host = bits16(inp["x"]) if wl.kind == "moe_w4a16" else codes8(inp["h" if wl.kind == "moe_fp8_w2" else "x"])
     sub = np.full_like(ids_np, -1)
     emap = {e: i for i, e in enumerate(experts)}
     for t in range(ids_np.shape[0]):
@@ -396,6 +401,8 @@ def test_moe_full_size(ops, key):
     ex_t = torch.tensor(experts, device="cuda")
     if wl.kind == "moe_fp8":
         ref = G.moe_w13_fp8(x_host, f32(inp["sx"]), codes8(inp["w"][ex_t]), f32(inp["sw"][ex_t]), sub, pairs=pairs)
+    elif wl.kind == "moe_fp8_w2":
+        ref = G.moe_w2_fp8(x_host, f32(inp["sh"]), codes8(inp["w"][ex_t]), f32(inp["sw"][ex_t]), sub, pairs=pairs)
     else:
         ref = G.moe_w13_w4a16(x_host, inp["w"][ex_t].cpu().numpy(), bits16(inp["ws"][ex_t]), sub, pairs=pairs)
     got = bf16_out(out)[pairs]
