@@ -42,7 +42,15 @@ static int cu_count() {
 // returns 1 if the shape is not covered (the caller then uses the per-unit
 // kernel), else the launch status.  KS = K-steps per wave = K / 128 / NW.
 template <int F, int EPI, int RB, int D, int NW = 8>
-static int try_stream(const SkinnyArgs& a, int dense_tiles, int max_tiles, hipStream_t st) {
+static int try_stream(const SkinnyArgs& a_in, int dense_tiles, int max_tiles, hipStream_t st) {
+  // A unit is RB 16-row blocks (SiLU: one gate and one up block, RB = 2), so
+  // the unit count per token tile follows from RB here rather than from the
+  // caller (whose units_n sizes the per-unit fallback kernel).
+  const int unit_rows = EPI == kSilu ? 16 : 16 * RB;
+  const int out_rows = EPI == kSilu ? a_in.N / 2 : a_in.N;
+  if (out_rows % unit_rows != 0) return 1;
+  SkinnyArgs a = a_in;
+  a.units_n = out_rows / unit_rows;
   // bf16 dense split-K: each work item covers K / nsplit (see stream_gemm_kernel)
   const int nsplit = (F == kBF16 && a.tiles == nullptr && a.partial != nullptr) ? a.ksplit : 1;
   if (nsplit < 1) return 1;
@@ -275,7 +283,7 @@ int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, cons
 #define STREAM_W2_CFG 1, 6, 8
 #endif
   constexpr int kCfg[] = {STREAM_W2_CFG};  // RB, D, NW
-  a.units_n = N / (16 * kCfg[0]);
+  a.units_n = N / (16 * kCfg[0]);  // the per-unit fallback below uses the same RB
   const int rc = try_stream<kFP8, kStore, STREAM_W2_CFG>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, max_tiles, st);
