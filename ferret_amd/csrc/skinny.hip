@@ -25,17 +25,18 @@
 
 namespace ferret {
 
-// Compute units of the current device (the persistent grid size).
+// Compute units of the current device (the persistent grid size), cached per
+// device; concurrent first calls store the same value.
 static int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Stream-kernel launch (persistent grid, one work-group of NW waves per CU):
