@@ -204,7 +204,14 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
     a.partial = nullptr;
     a.ksplit = 0;
   }
-  const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
+  // Unsplit: with >= 4 row units per CU, 4 waves of 8 K-steps per unit stream
+  // faster than 8 waves of 4 (the work-group's units start sooner and reduce
+  // over half the waves): GateUp 39.6 -> 36.7 us, LMHead 202 -> 195 us; with one
+  // unit per CU (O) 8 waves keep more bytes in flight.
+  const long long units = (long long)((M + 15) / 16) * (N / 16);
+  int rc = 1;
+  if (units >= 4LL * cu_count()) rc = try_stream<kBF16, kStore, 1, 4, 4>(a, (M + 15) / 16, 0, st);
+  if (rc == 1) rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
   if (rc != 1) return rc;
   return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, st);
 }

@@ -44,7 +44,9 @@ def test_single_hip_runtime(hip):
 
 @pytest.mark.parametrize("M,N,K,res", [(1, 64, 128, False), (5, 256, 512, True), (16, 512, 4096, False),
                                        (16, 128, 12288, True), (20, 96, 1024, False), (3, 48, 896, True),
-                                       (20, 256, 4096, False), (9, 1024, 7168, False), (33, 48, 4096, False)])
+                                       (20, 256, 4096, False), (9, 1024, 7168, False), (33, 48, 4096, False),
+                                       # >= 4 row units per CU: the 4-wave stream units (+ residual, K = 1024 / 3584)
+                                       (3, 16384, 1024, True), (16, 20480, 3584, False), (1, 16384, 4096, True)])
 def test_linear_bf16_small(ops, M, N, K, res):
     _say(f"linear_bf16 M={M} N={N} K={K} res={res}")
     g = torch.Generator(device="cuda").manual_seed(M * 1000 + N + K)
