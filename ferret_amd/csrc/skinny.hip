@@ -1,9 +1,10 @@
 // Skinny (<= 16 token) weight-streaming GEMMs for gfx950: bf16 decode linear,
-// small-M FP8 block-scaled GEMM, and the decode-sized MoE w13 grouped GEMMs
-// (FP8 block-scaled and INT4 W4A16) with the fused SiLU(gate)*up epilogue.
-// Shapes with K = 1024 * {4, 7, 8} (and no residual) run the persistent
-// LDS-staged stream kernel of stream_kernel.hpp; the per-unit kernel below
-// takes the rest.
+// small-M FP8 block-scaled GEMM, and the decode-sized MoE grouped GEMMs (FP8
+// w13 and w2, INT4 W4A16 w13) with the fused SiLU(gate)*up epilogue.  Shapes
+// whose K-steps split evenly into 2, 4, 7 or 8 per wave run the persistent
+// LDS-staged stream kernel of stream_kernel.hpp (bf16 with K split over a
+// workspace where the row units alone would leave CUs idle); the per-unit
+// kernel below takes the rest.
 //
 // Design (swap-AB): the weight rows are the MFMA "A" side (16 rows per MFMA)
 // and the <= 16 tokens of a unit are the MFMA "B" side, so a 16x16 MFMA tile
