@@ -11,7 +11,8 @@ permute + grouped GEMM (w13 or w2) for the MoE workloads; one quantizer or
 combine launch for those two workloads.  Weights of the dense workloads are
 rotated over enough copies (>= 512 MB) that no step finds its operands in the
 256 MB MALL.  `roofline` is measured live with HIP events on the launch stream
-around the dominant kernel; `cpu_baseline` times the CPU oracle on a bounded
+around the dominant kernel (around each GEMM for the MoE workloads, whose steps
+also route; around the whole run of back-to-back launches otherwise); `cpu_baseline` times the CPU oracle on a bounded
 sample of the same workload on this host and checks the GPU result against it.
 
 Ferret scoring mode (the reference's KERNEL_RESULT protocol, task_spec.py:277-356):
@@ -329,15 +330,30 @@ def time_steps(runner, steps: int, warmup: int):
     for i in range(warmup):
         runner.step(i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    if runner.wl.kind in MOE_KINDS:
+        # route + permute precede the GEMM in every step: one event pair per
+        # step brackets the GEMM alone
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            runner.step(warmup + i, evs[i])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return wall * 1e3 / steps, statistics.mean(s.elapsed_time(e) for s, e in evs)
+    # A step is one launch: one event pair around the back-to-back launches of
+    # all steps (each on its own weight copy).  Per-launch pairs would add the
+    # event records' own few microseconds to every launch of a ~10 us kernel.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for i in range(steps):
-        runner.step(warmup + i, evs[i])
+        runner.step(warmup + i)
+    ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = statistics.mean(s.elapsed_time(e) for s, e in evs)
-    return wall * 1e3 / steps, kernel_ms
+    return wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps
 
 
 def driver_mode(args) -> int:

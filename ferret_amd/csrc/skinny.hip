@@ -242,8 +242,18 @@ int ferret_fp8_gemm_skinny(const void* a_, const float* sa, const void* b, const
   // Short K (<= 2 K-steps per wave, e.g. K = 2048): two row blocks per unit
   // halve the per-unit reductions (o_proj, K = 2048: 8.2 -> 7.5 us); at K = 7168
   // one block with a deeper ring is faster (12.2 vs 13.5 us).
-  const int rc = (K >> 7) <= 16 ? try_stream<kFP8, kStore, 2, 3, 8>(a, (M + 15) / 16, 0, st)
-                                : try_stream<kFP8, kStore, STREAM_FP8_CFG>(a, (M + 15) / 16, 0, st);
+  // With at most one 16-row unit per CU (M = 16, N = 4096, K = 7168: 256 units)
+  // the whole unit is requested up front, so more waves per unit, each with
+  // fewer K-steps, shorten the first-byte-to-last-byte time: 14 waves x 4
+  // K-steps (ring depth 4) run 9.0 us against 10.0 us for 8 x 7.
+  const long long units16 = (long long)((M + 15) / 16) * (N / 16);
+  int rc = 1;
+  if ((K >> 7) <= 16) {
+    rc = try_stream<kFP8, kStore, 2, 3, 8>(a, (M + 15) / 16, 0, st);
+  } else {
+    if ((K >> 7) % 14 == 0 && units16 <= cu_count()) rc = try_stream<kFP8, kStore, 1, 4, 14>(a, (M + 15) / 16, 0, st);
+    if (rc == 1) rc = try_stream<kFP8, kStore, STREAM_FP8_CFG>(a, (M + 15) / 16, 0, st);
+  }
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, (M + 15) / 16, st);
 }

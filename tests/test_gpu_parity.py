@@ -123,7 +123,7 @@ def _fp8_inputs(M, N, K, seed):
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 128), (16, 256, 1024), (7, 4096, 7168), (17, 128, 512),
                                    (128, 256, 1024), (200, 384, 896), (256, 512, 7168),
-                                   (3, 384, 2048), (16, 128, 2048)])
+                                   (3, 384, 2048), (16, 128, 2048), (16, 256, 3584)])
 def test_fp8_gemm_small(ops, M, N, K):
     _say(f"fp8_gemm M={M} N={N} K={K}")
     a, sa, b, sb = _fp8_inputs(M, N, K, seed=M + N + K)
