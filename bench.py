@@ -23,7 +23,9 @@ Ferret scoring mode (the reference's KERNEL_RESULT protocol, task_spec.py:277-35
 prints `KERNEL_RESULT {...}` (GPU TFLOPS per config, 0.0 when the result fails
 the oracle check), `KERNEL_RESULT_REFERENCE {...}` (CPU fp32 oracle TFLOPS,
 same run) and `ROOFLINE {...}` (GB/s, TFLOPS, roofline fraction), timed the
-reference's way: a >= 512 MB flush before every timed iteration, >= 2 s of
+reference's way: a >= 512 MB flush before every timed iteration (a write, then a
+read of a second buffer so the write-back of the zeroed lines ends before the
+timed launch; --flush-read 0 keeps the write alone), >= 2 s of
 warmup, median of `--iters` event-timed iterations.
 """
 from __future__ import annotations
@@ -448,6 +450,9 @@ def kernel_result_mode(args) -> int:
 
     keys = FAMILIES[args.kernel_result]
     flush = torch.empty(args.flush_mb << 20, dtype=torch.uint8, device="cuda")
+    # Read after the write: the zeroed lines sit dirty in L2 / MALL, and without
+    # this pass their write-back would run inside the next timed GEMM.
+    flush_rd = torch.ones(args.flush_mb << 18, dtype=torch.int32, device="cuda") if args.flush_read else None
     res, ref, roof = {}, {}, {}
     for key in keys:
         wl = W.WORKLOADS[key]
@@ -463,6 +468,8 @@ def kernel_result_mode(args) -> int:
         times = []
         for _ in range(args.iters):
             flush.zero_()
+            if flush_rd is not None:
+                flush_rd.max()
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
             runner.gemm(0)
@@ -502,6 +509,8 @@ def main(argv=None) -> int:
     ap.add_argument("--iters", type=int, default=300)
     ap.add_argument("--warmup-s", type=float, default=2.0)
     ap.add_argument("--flush-mb", type=int, default=512)
+    ap.add_argument("--flush-read", type=int, default=1,
+                    help="after the flush write, read a second buffer of the same size (1) or not (0)")
     ap.add_argument("--launch-only", type=int, default=0, metavar="N",
                     help="only launch the workload's GEMM N times (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",
