@@ -302,11 +302,13 @@ int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, cons
   a.N = N;
   a.K = K;
   if (max_tiles <= 0) return FERRET_OK;
-// Two 16-row blocks per unit: K = 2048 gives each wave only 2 K-steps per
-// unit, so halving the units (and their cross-wave reductions) pays: 32
-// experts x 1 row 79 -> 71 us, 256 experts 605 -> 592 us.
+// K = 2048 gives 8 waves only 2 K-steps per 16-row unit, so wider units with
+// fewer waves pay (fewer cross-wave reductions per weight byte): two blocks
+// per unit took 32 experts x 1 row 79 -> 71 us and 256 experts 605 -> 592 us;
+// four blocks on 4 waves of 4 K-steps take 256 experts 593 -> 555 us and
+// 32 experts x 16 rows 82 -> 79 us.
 #ifndef STREAM_W2_CFG
-#define STREAM_W2_CFG 2, 3, 8
+#define STREAM_W2_CFG 4, 3, 4
 #endif
   a.units_n = N / 16;  // units of the per-unit fallback (RB = 1); try_stream derives its own
   const int rc = try_stream<kFP8, kStore, STREAM_W2_CFG>(a, 0, max_tiles, st);
