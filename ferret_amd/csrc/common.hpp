@@ -28,6 +28,15 @@ struct IntC {
   static constexpr int value = V;
 };
 
+// f(IntC<0>{}), ..., f(IntC<N-1>{}) in order.
+template <int I, int N, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 // ---------------------------------------------------------------- conversions
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {

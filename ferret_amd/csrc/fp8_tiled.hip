@@ -97,7 +97,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
+// F8 = true multiplies the e4m3 bytes on the FP8 MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales) instead of widening them to
+// bf16: one MFMA per 16x16x128 block instead of four and no widening, but the
+// FP8 datapath aligns the products of a dot-product group to a narrow window,
+// which costs about 1e-5 of max|C| at K = 7168 (an opt-in instance, see
+// FERRET_FP8_MMA_E4M3).
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8 = false>
 __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   static_assert(!SILU || GROUPED, "the SiLU epilogue is the grouped w13 GEMM's");
   using C = TileCfg<WN>;
@@ -161,7 +167,9 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   // global chunk (l%8) ^ key(row), so every instruction reads eight complete
   // 128-B lines.
   const uint8_t* wbase = p.b + (size_t)e * N * K;
-  uint32_t goff[TB_LD_PER_WAVE];
+  // 64-bit: row * K reaches 2^32 at e.g. 2^19 rows of K = 8192 (only the
+  // pointers below live on into the loop).
+  size_t goff[TB_LD_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < TB_LD_PER_WAVE; ++i) {
     const int j = wave * TB_LD_PER_WAVE + i;
@@ -173,13 +181,13 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
         wrow = (row < TB_N / 2) ? nb * (TB_N / 2) + row : N / 2 + nb * (TB_N / 2) + (row - TB_N / 2);
       else
         wrow = min(nb * TB_N + row, N - 1);  // rows past N (last block) are loaded but never stored
-      goff[i] = (uint32_t)wrow * (uint32_t)K + chunk * 16;
+      goff[i] = (size_t)wrow * K + chunk * 16;
     } else {
       const int row = (j - C::kWInstr) * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ swz_key(row);
       const int t = min(row, nrows - 1);
       const int tok = GROUPED ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
-      goff[i] = (uint32_t)tok * (uint32_t)K + chunk * 16;
+      goff[i] = (size_t)tok * K + chunk * 16;
     }
   }
   // Per-lane source of each load instruction (weights or tokens), so the
@@ -273,6 +281,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   // of this wave that hold tokens (a partial tile of a grouped GEMM skips the
   // empty ones; MI is uniform per wave).
   bf16x8 abf[4][4], wbf[4][4];
+  i32x8 araw[4], wraw[4];  // F8: the raw e4m3 bytes of each fragment
   float sa_v[4], sbg = 0.f, sbu = 0.f;
   auto phase_x = [&](auto mic, int step) {
     constexpr int MI = decltype(mic)::value;
@@ -293,6 +302,10 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       const int key = swz_key(t);
       const u32x4 lo = *reinterpret_cast<const u32x4*>(arow + (((2 * g) ^ key) << 4));
       const u32x4 hi = *reinterpret_cast<const u32x4*>(arow + (((2 * g + 1) ^ key) << 4));
+      if constexpr (F8) {
+        araw[mi] = cat_i32x8(lo, hi);
+        continue;
+      }
       abf[mi][0] = e4m3x8_to_bf16x8(lo[0], lo[1]);
       abf[mi][1] = e4m3x8_to_bf16x8(lo[2], lo[3]);
       abf[mi][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
@@ -303,6 +316,10 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       const int rr = wfrag_row[ni];
       const u32x4 lo = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g));
       const u32x4 hi = *reinterpret_cast<const u32x4*>(base + swz(rr, 2 * g + 1));
+      if constexpr (F8) {
+        wraw[ni] = cat_i32x8(lo, hi);
+        continue;
+      }
       wbf[ni][0] = e4m3x8_to_bf16x8(lo[0], lo[1]);
       wbf[ni][1] = e4m3x8_to_bf16x8(lo[2], lo[3]);
       wbf[ni][2] = e4m3x8_to_bf16x8(hi[0], hi[1]);
@@ -312,7 +329,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     // past the copy branches into Y, where they queue behind the same wave's
     // MFMAs instead of overlapping the partner wave's (8 % of the M = 4096
     // GEMM; the 4-wave tiles are faster unpinned).
-    if constexpr (WN == 4) {
+    if constexpr (WN == 4 && !F8) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -361,8 +378,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         f32x4 part = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (F8) {
+          part = mfma_fp8_16x16x128(wraw[ni], araw[mi], part);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[ni][j], abf[mi][j], part);
+          for (int j = 0; j < 4; ++j) part = mfma_bf16(wbf[ni][j], abf[mi][j], part);
+        }
         const float sc = sa_v[mi] * sbv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[ni][mi][i] = fmaf(part[i], sc, acc[ni][mi][i]);
@@ -499,12 +520,20 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
-template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
-static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st) {
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8>
+static int launch_tiled_one(const TiledArgs& p, dim3 grid, hipStream_t st) {
   using C = TileCfg<WN>;
-  FERRET_HIP_CHECK((set_lds_limit_once<fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>>(C::kLds)));
-  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL>), grid, dim3(C::kThreads), C::kLds, st, p);
+  FERRET_HIP_CHECK((set_lds_limit_once<fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8>>(C::kLds)));
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8>), grid, dim3(C::kThreads), C::kLds, st,
+                     p);
   return (int)hipGetLastError();
+}
+
+// f8: the FP8-MFMA instance (FERRET_FP8_MMA_E4M3), else the exact bf16 one.
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
+static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st, bool f8) {
+  return f8 ? launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, true>(p, grid, st)
+            : launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, false>(p, grid, st);
 }
 
 // Split-K plan for small M: 128 x 128 tiles (4 waves) over K ranges, the
@@ -532,7 +561,7 @@ size_t ferret_fp8_gemm_workspace(int M, int N, int K) {
 }
 
 int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const float* sb, void* c, int M,
-                          int N, int K, void* ws, size_t ws_bytes, hipStream_t st) {
+                          int N, int K, void* ws, size_t ws_bytes, bool f8, hipStream_t st) {
   TiledArgs p{};
   p.a = static_cast<const uint8_t*>(a);
   p.sa = sa;
@@ -552,8 +581,8 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     p.partial = static_cast<float*>(ws);
     p.n_blocks = N / (64 * SPLITK_WN);
     const dim3 grid(p.n_blocks * p.m_blocks, used);
-    const int rc = M % TB_M == 0 ? launch_tiled<false, false, SPLITK_WN, true, true>(p, grid, st)
-                                 : launch_tiled<false, false, SPLITK_WN, true, false>(p, grid, st);
+    const int rc = M % TB_M == 0 ? launch_tiled<false, false, SPLITK_WN, true, true>(p, grid, st, f8)
+                                 : launch_tiled<false, false, SPLITK_WN, true, false>(p, grid, st, f8);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
@@ -563,13 +592,13 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
   // Dense tiles: with every token tile full (M % 128 == 0) the kernel skips
   // the per-wave count of occupied 16-token sub-tiles.
   p.n_blocks = (N + 255) / 256;
-  if (M % TB_M == 0) return launch_tiled<false, false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st);
-  return launch_tiled<false, false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st);
+  if (M % TB_M == 0) return launch_tiled<false, false, 4, false, true>(p, dim3(p.n_blocks * p.m_blocks), st, f8);
+  return launch_tiled<false, false, 4, false, false>(p, dim3(p.n_blocks * p.m_blocks), st, f8);
 }
 
 int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, const float* sw,
                              const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
-                             int max_tiles, int topk, int N, int K, void* out, hipStream_t st) {
+                             int max_tiles, int topk, int N, int K, void* out, bool f8, hipStream_t st) {
   TiledArgs p{};
   p.a = static_cast<const uint8_t*>(x);
   p.sa = sx;
@@ -586,14 +615,14 @@ int ferret_moe_w13_fp8_tiled(const void* x, const float* sx, const void* w, cons
   const long long grid = (long long)max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
   if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
-  return launch_tiled<true, true, 4, false, false>(p, dim3((unsigned)grid), st);
+  return launch_tiled<true, true, 4, false, false>(p, dim3((unsigned)grid), st, f8);
 }
 
 // Prefill-sized MoE w2 / down projection: grouped tiles, bf16 store to the
 // routed pair's row; the A row of a sorted row is its pair too (topk = 1).
 int ferret_moe_w2_fp8_tiled(const void* h, const float* sh, const void* w, const float* sw,
                             const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
-                            int max_tiles, int N, int K, void* out, hipStream_t st) {
+                            int max_tiles, int N, int K, void* out, bool f8, hipStream_t st) {
   TiledArgs p{};
   p.a = static_cast<const uint8_t*>(h);
   p.sa = sh;
@@ -610,5 +639,5 @@ int ferret_moe_w2_fp8_tiled(const void* h, const float* sh, const void* w, const
   const long long grid = (long long)max_tiles * p.n_blocks;
   if (grid <= 0) return FERRET_OK;
   if (grid >= (1LL << 31)) return FERRET_ERR_SHAPE;
-  return launch_tiled<false, true, 4, false, false>(p, dim3((unsigned)grid), st);
+  return launch_tiled<false, true, 4, false, false>(p, dim3((unsigned)grid), st, f8);
 }

@@ -100,15 +100,6 @@ __device__ __forceinline__ void wait_items(int n) {
   }
 }
 
-// f(IntC<0>{}), ..., f(IntC<N-1>{}) in order.
-template <int I, int N, typename Fn>
-__device__ __forceinline__ void static_for(Fn&& f) {
-  if constexpr (I < N) {
-    f(IntC<I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 // s_waitcnt lgkmcnt(0) only (LDS writes done before a barrier).
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 

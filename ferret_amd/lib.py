@@ -35,8 +35,18 @@ SIGNATURES = {
     "ferret_moe_w2_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _vp, _vp]),
     "ferret_moe_combine": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "ferret_fp8_gemm_blockscale_ex": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t,
+                                               _c_int, _vp]),
+    "ferret_moe_w13_fp8_ex": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _c_int, _vp, _c_int, _vp]),
+    "ferret_moe_w2_fp8_ex": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _c_int, _vp, _c_int, _vp]),
     "ferret_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
 }
+
+
+# Flag bits of the FP8 *_ex entry points (include/ferret_hip.h).
+FP8_MMA_E4M3 = 1
 
 
 class FerretError(RuntimeError):

@@ -72,13 +72,23 @@ def fp8_workspace_bytes(M: int, N: int, K: int) -> int:
     return int(_lib.load().ferret_workspace_bytes(1, M, N, K, 0))
 
 
+def _mma_flags(mma: str) -> int:
+    if mma == "bf16":
+        return 0
+    if mma == "e4m3":
+        return _lib.FP8_MMA_E4M3
+    raise ValueError(f"mma must be 'bf16' (exact widening, the default) or 'e4m3' (FP8 MFMA), got {mma!r}")
+
+
 def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
-                        out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                        out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                        mma: str = "bf16") -> torch.Tensor:
     """c[M,N] (bf16) = block-scaled a[M,K] (e4m3) . b[N,K]^T (e4m3).
 
     Shapes with M <= 256 run split-K over a workspace; pass one of at least
     fp8_workspace_bytes(M, N, K) bytes to reuse it across calls (else one is
-    taken from torch's caching allocator).
+    taken from torch's caching allocator).  mma="e4m3" opts the tiled (M > 16)
+    kernels into the FP8 MFMA (FERRET_FP8_MMA_E4M3: faster, less precise).
     """
     M, K = a.shape
     N = b.shape[0]
@@ -92,9 +102,10 @@ def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: 
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
     ws_ptr = _dev(workspace, "workspace") if need else None
-    rc = _lib.load().ferret_fp8_gemm_blockscale(
+    rc = _lib.load().ferret_fp8_gemm_blockscale_ex(
         _dev(a, "a", (FP8, torch.uint8), 2), _dev(sa, "sa", torch.float32, 2), _dev(b, "b", (FP8, torch.uint8), 2),
-        _dev(sb, "sb", torch.float32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K, ws_ptr, need, _stream())
+        _dev(sb, "sb", torch.float32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K, ws_ptr, need,
+        _mma_flags(mma), _stream())
     _lib.check("ferret_fp8_gemm_blockscale", rc)
     return out
 
@@ -163,7 +174,7 @@ def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int | None = None,
 
 
 def moe_w13_fp8(x: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, routing: Routing,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, mma: str = "bf16") -> torch.Tensor:
     """out[P, N/2] bf16 = silu(gate) * up of the FP8 block-scaled w13 projection."""
     T, K = x.shape
     E, N, K2 = w.shape
@@ -174,11 +185,11 @@ def moe_w13_fp8(x: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, sw: torch.Te
     P = T * routing.topk
     if out is None:
         out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
-    rc = _lib.load().ferret_moe_w13_fp8(
+    rc = _lib.load().ferret_moe_w13_fp8_ex(
         _dev(x, "x", (FP8, torch.uint8), 2), _dev(sx, "sx", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
         _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
         routing.ntiles.data_ptr(), routing.max_tiles, routing.tile_m, T, routing.topk, E, N, K,
-        _dev(out, "out", torch.bfloat16, 2), _stream())
+        _dev(out, "out", torch.bfloat16, 2), _mma_flags(mma), _stream())
     _lib.check("ferret_moe_w13_fp8", rc)
     return out
 
@@ -217,7 +228,7 @@ def quant_act_e4m3(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.
 
 
 def moe_w2_fp8(h: torch.Tensor, sh: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, routing: Routing,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, mma: str = "bf16") -> torch.Tensor:
     """out[P, N] bf16 (pair order) = the FP8 block-scaled down projection of h [P, K] (pair order)."""
     P, K = h.shape
     E, N, K2 = w.shape
@@ -227,11 +238,11 @@ def moe_w2_fp8(h: torch.Tensor, sh: torch.Tensor, w: torch.Tensor, sw: torch.Ten
         raise ValueError("scale shapes must be sh [P, K/128], sw [E, N/128, K/128]")
     if out is None:
         out = torch.empty((P, N), dtype=torch.bfloat16, device=h.device)
-    rc = _lib.load().ferret_moe_w2_fp8(
+    rc = _lib.load().ferret_moe_w2_fp8_ex(
         _dev(h, "h", (FP8, torch.uint8), 2), _dev(sh, "sh", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
         _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
         routing.ntiles.data_ptr(), routing.max_tiles, routing.tile_m, P, E, N, K,
-        _dev(out, "out", torch.bfloat16, 2), _stream())
+        _dev(out, "out", torch.bfloat16, 2), _mma_flags(mma), _stream())
     _lib.check("ferret_moe_w2_fp8", rc)
     return out
 

@@ -189,6 +189,35 @@ int ferret_moe_w2_fp8(const void* h, const float* sh, const void* w, const float
  */
 int ferret_moe_combine(const void* o, const float* w, int T, int topk, int N, void* y, void* stream);
 
+/*
+ * Flags of the FP8 *_ex entry points below.  FERRET_FP8_MMA_E4M3 multiplies
+ * the e4m3 operands of the tiled (M > 16 / prefill) kernels on the FP8 MFMA
+ * (v_mfma_scale_f32_16x16x128_f8f6f4) instead of widening them exactly to
+ * bf16: one MFMA per 16x16x128 block instead of four, but the FP8 datapath
+ * aligns the products of each dot-product group to a narrow window, so the
+ * result can miss the reference's gate |g - r| / max(|r|, 1e-3 max|r|) < 1e-2
+ * (examples/fp8-gemm/v002_dense_tp8_validated_065.cu:345-360) that the default
+ * path meets.  Opt-in only; decode-sized (<= 16 token) shapes ignore it.
+ */
+#define FERRET_FP8_MMA_E4M3 1
+
+/* ferret_fp8_gemm_blockscale with flags (0 = the same as the plain call). */
+int ferret_fp8_gemm_blockscale_ex(const void* a, const float* sa, const void* b, const float* sb,
+                                  void* c, int M, int N, int K, void* ws, size_t ws_bytes, int flags,
+                                  void* stream);
+
+/* ferret_moe_w13_fp8 with flags (0 = the same as the plain call). */
+int ferret_moe_w13_fp8_ex(const void* x, const float* sx, const void* w, const float* sw,
+                          const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                          int max_tiles, int tile_m, int T, int topk, int E, int N, int K, void* out,
+                          int flags, void* stream);
+
+/* ferret_moe_w2_fp8 with flags (0 = the same as the plain call). */
+int ferret_moe_w2_fp8_ex(const void* h, const float* sh, const void* w, const float* sw,
+                         const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                         int max_tiles, int tile_m, int P, int E, int N, int K, void* out, int flags,
+                         void* stream);
+
 /* Workspace bytes an op can use (0 = none). op: 0 linear_bf16 (split-K partials),
  * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
  * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts). */
