@@ -540,12 +540,8 @@ static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st, bool f8) 
 // number of splits doubled until the grid covers the 256 CUs once (measured
 // on 128 x 4096 x 7168 against 64 x 128 and 256 x 128 tiles and 2 grids per
 // CU: 28 us vs 29-36 us).  Returns the number of splits (1 = no split-K).
-#ifndef SPLITK_WN
-#define SPLITK_WN 2
-#endif
-#ifndef SPLITK_TARGET
-#define SPLITK_TARGET 256
-#endif
+constexpr int SPLITK_WN = 2;         // 128 x 128 tiles (4 waves)
+constexpr int SPLITK_TARGET = 256;   // work-groups the split grid should reach
 static int splitk_splits(int M, int N, int K) {
   if (M > 256 || N % (64 * SPLITK_WN) != 0) return 1;
   const int tiles = (N / (64 * SPLITK_WN)) * ((M + TB_M - 1) / TB_M);

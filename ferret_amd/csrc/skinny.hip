@@ -185,15 +185,12 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   a.N = N;
   a.K = K;
   a.units_n = N / 16;
-#ifndef STREAM_BF16_CFG
-#define STREAM_BF16_CFG 1, 3, 8
-#endif
   const int splits = linear_splits(M, N, K);
   const size_t need = ferret_linear_bf16_workspace(M, N, K);
   if (splits > 1 && ws != nullptr && ws_bytes >= need && (M * (long long)N) % 4 == 0) {
     a.partial = static_cast<float*>(ws);
     a.ksplit = splits;
-    const int rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
+    const int rc = try_stream<kBF16, kStore, 1, 3, 8>(a, (M + 15) / 16, 0, st);
     if (rc != 1) {
       if (rc != 0) return rc;
       const long long mn4 = (long long)M * N / 4;
@@ -212,7 +209,7 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   const long long units = (long long)((M + 15) / 16) * (N / 16);
   int rc = 1;
   if (units >= 4LL * cu_count()) rc = try_stream<kBF16, kStore, 1, 4, 4>(a, (M + 15) / 16, 0, st);
-  if (rc == 1) rc = try_stream<kBF16, kStore, STREAM_BF16_CFG>(a, (M + 15) / 16, 0, st);
+  if (rc == 1) rc = try_stream<kBF16, kStore, 1, 3, 8>(a, (M + 15) / 16, 0, st);
   if (rc != 1) return rc;
   return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, st);
 }
@@ -236,9 +233,6 @@ int ferret_fp8_gemm_skinny(const void* a_, const float* sa, const void* b, const
   a.N = N;
   a.K = K;
   a.units_n = N / 16;  // units of the per-unit fallback (RB = 1)
-#ifndef STREAM_FP8_CFG
-#define STREAM_FP8_CFG 1, 6, 8
-#endif
   // Short K (<= 2 K-steps per wave, e.g. K = 2048): two row blocks per unit
   // halve the per-unit reductions (o_proj, K = 2048: 8.2 -> 7.5 us); at K = 7168
   // one block with a deeper ring is faster (12.2 vs 13.5 us).
@@ -252,7 +246,7 @@ int ferret_fp8_gemm_skinny(const void* a_, const float* sa, const void* b, const
     rc = try_stream<kFP8, kStore, 2, 3, 8>(a, (M + 15) / 16, 0, st);
   } else {
     if ((K >> 7) % 14 == 0 && units16 <= cu_count()) rc = try_stream<kFP8, kStore, 1, 4, 14>(a, (M + 15) / 16, 0, st);
-    if (rc == 1) rc = try_stream<kFP8, kStore, STREAM_FP8_CFG>(a, (M + 15) / 16, 0, st);
+    if (rc == 1) rc = try_stream<kFP8, kStore, 1, 6, 8>(a, (M + 15) / 16, 0, st);
   }
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, (M + 15) / 16, st);
@@ -276,10 +270,7 @@ int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, con
   a.K = K;
   a.units_n = N / 32;
   if (max_tiles <= 0) return FERRET_OK;
-#ifndef STREAM_MOE_CFG
-#define STREAM_MOE_CFG 2, 3, 8
-#endif
-  const int rc = try_stream<kFP8, kSilu, STREAM_MOE_CFG>(a, 0, max_tiles, st);
+  const int rc = try_stream<kFP8, kSilu, 2, 3, 8>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kSilu, 2>(a, max_tiles, st);
 }
@@ -307,11 +298,8 @@ int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, cons
 // per unit took 32 experts x 1 row 79 -> 71 us and 256 experts 605 -> 592 us;
 // four blocks on 4 waves of 4 K-steps take 256 experts 593 -> 555 us and
 // 32 experts x 16 rows 82 -> 79 us.
-#ifndef STREAM_W2_CFG
-#define STREAM_W2_CFG 4, 3, 4
-#endif
   a.units_n = N / 16;  // units of the per-unit fallback (RB = 1); try_stream derives its own
-  const int rc = try_stream<kFP8, kStore, STREAM_W2_CFG>(a, 0, max_tiles, st);
+  const int rc = try_stream<kFP8, kStore, 4, 3, 4>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
   return launch_skinny<kFP8, kStore, 1>(a, max_tiles, st);
 }
@@ -336,10 +324,7 @@ extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void
   a.K = K;
   a.units_n = N / 32;
   if (max_tiles <= 0) return FERRET_OK;
-#ifndef STREAM_INT4_CFG
-#define STREAM_INT4_CFG 2, 5, 8
-#endif
-  const int rc = try_stream<kINT4, kSilu, STREAM_INT4_CFG>(a, 0, max_tiles, (hipStream_t)stream);
+  const int rc = try_stream<kINT4, kSilu, 2, 5, 8>(a, 0, max_tiles, (hipStream_t)stream);
   if (rc != 1) return rc;
   return launch_skinny<kINT4, kSilu, 2>(a, max_tiles, (hipStream_t)stream);
 }
