@@ -214,6 +214,51 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
   return launch_skinny<kBF16, kStore, 1>(a, (M + 15) / 16, st);
 }
 
+// ---- allocation-free decode linear (no counterpart in the reference).
+// Callers that cannot allocate (code under HIP graph capture, serving loops)
+// get the split-K partials of ferret_linear_bf16 from this file-scope device
+// array instead of a workspace argument.  Each GPU holds its own copy until
+// the process ends; its address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// handed to kernels.  Calls that overlap on one GPU share the array and race;
+// every split writes all of its partials before the reduce reads them, so
+// nothing needs clearing between calls.
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::atomic<void*> g_scratch_ptr[64];
+
+// Device address of `scratch` on the current device (cached per device), or
+// the hipGetSymbolAddress error.
+static hipError_t scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return hipSuccess;
+}
+
+extern "C" size_t ferret_linear_bf16_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int ferret_linear_bf16_noalloc(const void* x, const void* w, const void* residual, void* y, int M,
+                                          int N, int K, void* stream) {
+  FERRET_REQUIRE(x && w && y, FERRET_ERR_NULL);
+  FERRET_REQUIRE(M >= 1 && N >= 16 && K >= 128, FERRET_ERR_SHAPE);
+  FERRET_REQUIRE(N % 16 == 0 && K % 128 == 0 && K / 128 <= 128, FERRET_ERR_SHAPE);
+  const size_t need = ferret_linear_bf16_workspace(M, N, K);
+  FERRET_REQUIRE(need <= kNoAllocScratchBytes, FERRET_ERR_WORKSPACE);
+  void* ws = nullptr;
+  if (need > 0) FERRET_HIP_CHECK(scratch_address(&ws));
+  return ferret_linear_bf16(x, w, residual, y, M, N, K, ws, need, stream);
+}
+
 extern "C" void launch_gemv(void* input, void* weight, void* residual, void* output, int N, int K,
                             void* stream) {
   (void)ferret_linear_bf16(input, weight, residual, output, 1, N, K, nullptr, 0, stream);

@@ -35,6 +35,8 @@ SIGNATURES = {
     "ferret_moe_w2_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _vp, _vp]),
     "ferret_moe_combine": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "ferret_linear_bf16_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "ferret_linear_bf16_noalloc_max_bytes": (_c_size_t, []),
     "ferret_fp8_gemm_blockscale_ex": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t,
                                                _c_int, _vp]),
     "ferret_moe_w13_fp8_ex": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,

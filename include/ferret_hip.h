@@ -65,6 +65,24 @@ int ferret_linear_bf16(const void* x, const void* w, const void* residual, void*
                        int K, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * ferret_linear_bf16 without a workspace argument and without any allocation:
+ * no counterpart in the reference.  For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Shapes that run split-K take their fp32 partials from a
+ * library-owned device array of ferret_linear_bf16_noalloc_max_bytes()
+ * (4 MiB) per GPU; a shape needing more (ferret_workspace_bytes(0, M, N, K, 0)
+ * larger than that) is rejected with FERRET_ERR_WORKSPACE.  The result is
+ * bit-identical to ferret_linear_bf16 with a workspace.  Calls that overlap on
+ * one GPU (different streams or threads) share the array and race: serialise
+ * them.  The first call on each device looks the array's address up once.
+ */
+int ferret_linear_bf16_noalloc(const void* x, const void* w, const void* residual, void* y, int M,
+                               int N, int K, void* stream);
+
+/* Bytes of the device array ferret_linear_bf16_noalloc uses (its limit). */
+size_t ferret_linear_bf16_noalloc_max_bytes(void);
+
+/*
  * Dense FP8 GEMM with DeepSeek-style fp32 block scales:
  *   c[m,n] = sum_kb (sum_{k in kb} a[m,k] b[n,k]) * sa[m,kb] * sb[n/128,kb]
  * a e4m3 [M,K], sa f32 [M,K/128], b e4m3 [N,K], sb f32 [ceil(N/128),K/128],

@@ -71,6 +71,20 @@ def test_argument_errors_are_returned_not_raised_without_gpu():
     assert L.ferret_moe_combine(1, 1, 4, 0, 128, 1, None) == -2
 
 
+def test_noalloc_linear_rejects_oversized_partials_without_gpu():
+    """ferret_linear_bf16_noalloc checks its array limit before any HIP call."""
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    L = lib.load()
+    assert L.ferret_linear_bf16_noalloc_max_bytes() == 4 << 20
+    assert L.ferret_linear_bf16_noalloc(None, 1, None, 1, 16, 4096, 4096, None) == -1
+    assert L.ferret_linear_bf16_noalloc(1, 1, None, 1, 16, 100, 4096, None) == -2
+    # M = 100, N = 4096, K = 12288 splits K three ways: 4.9 MB of partials
+    assert L.ferret_workspace_bytes(0, 100, 4096, 12288, 0) > 4 << 20
+    assert L.ferret_linear_bf16_noalloc(1, 1, None, 1, 100, 4096, 12288, None) == -3
+
+
 def test_python_ops_refuse_cpu_tensors():
     import torch
     from ferret_amd import ops
