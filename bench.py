@@ -13,8 +13,10 @@ rotated over enough copies (>= 512 MB) that no step finds its operands in the
 256 MB MALL.  `roofline` is measured live with HIP events on the launch stream
 around the dominant kernel (a pair around each launch and, for the single-launch
 workloads, also one pair around a burst of back-to-back launches; the smaller
-per-launch time is used and both are reported); `cpu_baseline` times the CPU oracle on a bounded
-sample of the same workload on this host and checks the GPU result against it.
+per-launch time is used and both are reported).  `cpu_baseline` checks the GPU
+result against the numpy oracle on a bounded sample of the workload and times
+the PyTorch-CPU fp32 dequantize-then-matmul path on that sample with the host's
+physical cores; every `also` workload carries the same oracle check.
 
 Ferret scoring mode (the reference's KERNEL_RESULT protocol, task_spec.py:277-356):
 
@@ -23,10 +25,11 @@ Ferret scoring mode (the reference's KERNEL_RESULT protocol, task_spec.py:277-35
 prints `KERNEL_RESULT {...}` (GPU TFLOPS per config, 0.0 when the result fails
 the oracle check), `KERNEL_RESULT_REFERENCE {...}` (CPU fp32 oracle TFLOPS,
 same run) and `ROOFLINE {...}` (GB/s, TFLOPS, roofline fraction), timed the
-reference's way: a >= 512 MB flush before every timed iteration (a write, then a
-read of a second buffer so the write-back of the zeroed lines ends before the
-timed launch; --flush-read 0 keeps the write alone), >= 2 s of
-warmup, median of `--iters` event-timed iterations.
+reference's way: a >= 512 MB write flush before every timed iteration (the
+reference's 128 MB zero_() flush enlarged past the 256 MB MALL), >= 2 s of
+warmup, median of `--iters` event-timed iterations.  --flush-read 1 adds a read
+of a second 512 MB buffer after the write (the zeroed lines' write-back then
+ends before the timed launch): a different protocol, labelled as such.
 """
 from __future__ import annotations
 
@@ -157,17 +160,38 @@ def unit_of(wl):
 
 
 def roofline_of(wl, runner, kernel_ms: float) -> dict:
+    """Achieved rate of the dominant kernel against its roofline.
+
+    `frac` is against the peak of the bound named (8 TB/s, or the FP8 / bf16
+    MFMA peak); `frac_attainable` against min(peak, AI x 8 TB/s) in the line's
+    unit (AI = algorithmic FLOP per algorithmic byte), which is what an
+    HBM-limited prefill shape can reach at best; `frac_bf16_peak` (FP8 kinds)
+    against the 2.5 PFLOP/s bf16 MFMA peak the exact-widening kernels run on.
+    """
     unit, bound = unit_of(wl)
+    ai = runner.flops / max(runner.bytes, 1)
+    fp8 = wl.kind in ("fp8_gemm", "moe_fp8", "moe_fp8_w2")
+    mfma_peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
+    tflops = runner.flops / (kernel_ms * 1e-3) / 1e12
+    gbps = runner.bytes / (kernel_ms * 1e-3) / 1e9
     if bound == "mfma":
-        achieved = runner.flops / (kernel_ms * 1e-3) / 1e12
-        peak = PEAK_FP8_TFLOPS if wl.kind in ("fp8_gemm", "moe_fp8", "moe_fp8_w2") else PEAK_BF16_TFLOPS
+        achieved, peak = tflops, mfma_peak
+        attainable = min(mfma_peak, ai * PEAK_HBM_GBPS / 1e3)
     else:
-        achieved = runner.bytes / (kernel_ms * 1e-3) / 1e9
-        peak = PEAK_HBM_GBPS
-    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic_of(wl.key),
-            "kernel_us": round(kernel_ms * 1e3, 3), "algorithmic_bytes": runner.bytes,
-            "flops": runner.flops}
+        achieved, peak = gbps, PEAK_HBM_GBPS
+        attainable = min(PEAK_HBM_GBPS, mfma_peak * 1e3 / max(ai, 1e-30))
+    out = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "attainable": round(attainable, 3),
+           "frac_attainable": round(achieved / attainable, 4), "ai_flop_per_byte": round(ai, 3),
+           "traffic": traffic_of(wl.key), "traffic_source": TRAFFIC_SOURCE,
+           "kernel_us": round(kernel_ms * 1e3, 3), "algorithmic_bytes": runner.bytes, "flops": runner.flops}
+    if fp8 and wl.kind != "quant_act":
+        out["frac_bf16_peak"] = round(tflops / PEAK_BF16_TFLOPS, 4)
+    return out
+
+
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of `bench.py --workload "
+                  "KEY --launch-only 3`, scaled by a copy kernel of known size (not measured in this run)")
 
 
 def traffic_of(key: str):
@@ -185,27 +209,33 @@ def traffic_of(key: str):
 
 # ---------------------------------------------------------------------------- CPU oracle leg
 
-def _blas_threads() -> int:
+def cpu_threads() -> dict:
+    """Threads for the PyTorch-CPU baseline: the host's physical cores, capped by
+    OMP_NUM_THREADS when the environment sets it (the CPU share of one GPU)."""
+    logical = os.cpu_count() or 1
     try:
-        from threadpoolctl import threadpool_info
-        n = [p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"]
-        return max(n) if n else 1
+        import psutil
+        physical = psutil.cpu_count(logical=False) or logical
     except Exception:
-        return 1
+        physical = logical
+    n = physical
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return {"threads": n, "physical_cores": physical, "os_cpu_count": logical}
 
 
-def cpu_baseline(wl, runner, budget_s: float = 12.0) -> dict:
-    """Time the CPU oracle on a bounded sample and check the GPU output on it.
+def _sample(wl, runner):
+    """A bounded sample of the workload for the CPU legs.
 
-    The sample is a subset of output rows (dense) or of routed experts (MoE)
-    that the oracle finishes in well under a second to a few seconds; it is
-    run repeatedly (at least 3 times) until about budget_s seconds of CPU work
-    are spent, and the throughput is that sample's FLOPs (and algorithmic
-    bytes) over the median run time.
+    Returns (oracle_fn, torch_fn, got, s_flops, s_bytes, description, exact):
+    oracle_fn runs the pinned numpy oracle (the correctness check), torch_fn the
+    PyTorch-CPU fp32 dequantize-then-matmul path (the timed baseline) on the same
+    sample, `got` the GPU result on it.
     """
     import numpy as np
     import torch
-    from oracle import formats as F, gemm as G, metrics as MT, quant as Q, routing as R
+    from oracle import formats as F, gemm as G, quant as Q, routing as R, torch_cpu as TC
 
     def bits16(t):
         return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
@@ -214,101 +244,120 @@ def cpu_baseline(wl, runner, budget_s: float = 12.0) -> dict:
         return t.contiguous().view(torch.uint8).cpu().numpy()
 
     inp, out = runner.inp, runner.output()
-    got_all = None if wl.kind == "quant_act" else F.bf16_bits_to_f32(bits16(out))
     rng = np.random.default_rng(0)
-    check = None   # exact comparison (quantizer) instead of the GEMM error metric
     if wl.kind == "quant_act":
         nrows = min(wl.M, 2048)
         rows = np.sort(rng.choice(wl.M, size=nrows, replace=False))
         xs = F.bf16_bits_to_f32(bits16(inp["x"])[rows])
-        fn = lambda: Q.quant_act_1x128(xs)  # noqa: E731
-        s_flops = 2 * nrows * wl.K
-        s_bytes = nrows * wl.K * 3 + nrows * (wl.K // 128) * 4
-        sample = f"{nrows} of {wl.M} rows"
-        gq, gs = codes(out[0])[rows], out[1].cpu().numpy()[rows]
-        check = lambda r: bool(np.array_equal(gq, r[0]) and np.array_equal(gs, r[1]))  # noqa: E731
-        got = None
-    elif wl.kind == "moe_combine":
+        got = (codes(out[0])[rows], out[1].cpu().numpy()[rows])
+        return (lambda: Q.quant_act_1x128(xs), lambda: TC.quant_act_1x128(xs), got, 2 * nrows * wl.K,
+                nrows * wl.K * 3 + nrows * (wl.K // 128) * 4, f"{nrows} of {wl.M} rows", True)
+    got_all = F.bf16_bits_to_f32(bits16(out))
+    if wl.kind == "moe_combine":
         ntok = min(wl.T, 1024)
         toks = np.sort(rng.choice(wl.T, size=ntok, replace=False))
         prow = (toks[:, None] * wl.topk + np.arange(wl.topk)[None, :]).reshape(-1)
         ob, wts = bits16(inp["o"])[prow], inp["w"].cpu().numpy()[toks]
-        fn = lambda: G.moe_combine(ob, wts)  # noqa: E731
-        s_flops = 2 * ntok * wl.topk * wl.N
-        s_bytes = ntok * wl.topk * (wl.N * 2 + 4) + ntok * wl.N * 2
-        sample = f"{ntok} of {wl.T} tokens x all {wl.N} columns"
-        got = got_all[toks]
-    elif wl.kind == "linear_bf16":
+        return (lambda: G.moe_combine(ob, wts), lambda: TC.moe_combine(ob, wts), got_all[toks],
+                2 * ntok * wl.topk * wl.N, ntok * wl.topk * (wl.N * 2 + 4) + ntok * wl.N * 2,
+                f"{ntok} of {wl.T} tokens x all {wl.N} columns", False)
+    if wl.kind == "linear_bf16":
         xb, wb = bits16(inp["x"]), bits16(inp["w"])
         rb = bits16(inp["r"]) if "r" in inp else None
-        rows = np.arange(wl.M)
-        fn = lambda: G.linear_bf16(xb, wb, rb)  # noqa: E731
-        s_flops = 2 * wl.M * wl.N * wl.K
-        s_bytes = runner.bytes
-        sample = f"all {wl.M} rows x {wl.N} outputs"
-        got = got_all
-    elif wl.kind == "fp8_gemm":
+        return (lambda: G.linear_bf16(xb, wb, rb), lambda: TC.linear_bf16(xb, wb, rb), got_all,
+                2 * wl.M * wl.N * wl.K, runner.bytes, f"all {wl.M} rows x {wl.N} outputs", False)
+    if wl.kind == "fp8_gemm":
         nrows = min(wl.M, 1024)
         rows = np.sort(rng.choice(wl.M, size=nrows, replace=False)) if nrows < wl.M else np.arange(wl.M)
         a, sa, b, sb = codes(inp["a"])[rows], inp["sa"].cpu().numpy()[rows], codes(inp["b"]), inp["sb"].cpu().numpy()
-        fn = lambda: G.fp8_blockscale_gemm(a, sa, b, sb)  # noqa: E731
-        s_flops = 2 * nrows * wl.N * wl.K
-        s_bytes = nrows * wl.K * 1 + wl.N * wl.K + nrows * wl.N * 2
-        sample = f"{nrows} of {wl.M} rows x all {wl.N} outputs"
-        got = got_all[rows]
+        return (lambda: G.fp8_blockscale_gemm(a, sa, b, sb), lambda: TC.fp8_blockscale_gemm(a, sa, b, sb),
+                got_all[rows], 2 * nrows * wl.N * wl.K, nrows * wl.K * 1 + wl.N * wl.K + nrows * wl.N * 2,
+                f"{nrows} of {wl.M} rows x all {wl.N} outputs", False)
+    ids = runner.ids.cpu().numpy()
+    counts, offsets, sp = R.permute(ids, wl.E)
+    hit = np.nonzero(counts)[0]
+    order = hit[np.argsort(counts[hit], kind="stable")]
+    nexp = 4
+    experts = sorted({int(order[0]), int(order[-1])} | {int(e) for e in rng.permutation(hit)[: nexp - 2]})
+    pairs = []
+    for e in experts:
+        seg = sp[offsets[e]:offsets[e + 1]]
+        pairs.extend(int(p) for p in (seg if len(seg) <= 256 else np.r_[seg[:128], seg[-128:]]))
+    pairs = np.array(pairs)
+    emap = {e: i for i, e in enumerate(experts)}
+    sub = np.vectorize(lambda v: emap.get(int(v), -1))(ids).astype(np.int32)
+    ex_t = torch.tensor(experts, device="cuda")
+    if wl.kind == "moe_fp8":
+        x, sx = codes(inp["x"]), inp["sx"].cpu().numpy()
+        w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
+        fo = lambda: G.moe_w13_fp8(x, sx, w, sw, sub, pairs=pairs)  # noqa: E731
+        ft = lambda: TC.moe_w13_fp8(x, sx, w, sw, sub, pairs)  # noqa: E731
+        per_e = wl.N * wl.K
+    elif wl.kind == "moe_fp8_w2":
+        h, sh = codes(inp["h"]), inp["sh"].cpu().numpy()
+        w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
+        fo = lambda: G.moe_w2_fp8(h, sh, w, sw, sub, pairs=pairs)  # noqa: E731
+        ft = lambda: TC.moe_w2_fp8(h, sh, w, sw, sub, pairs)  # noqa: E731
+        per_e = wl.N * wl.K
     else:
-        ids = runner.ids.cpu().numpy()
-        counts, offsets, sp = R.permute(ids, wl.E)
-        hit = np.nonzero(counts)[0]
-        order = hit[np.argsort(counts[hit], kind="stable")]
-        nexp = 4
-        experts = sorted({int(order[0]), int(order[-1])} | {int(e) for e in rng.permutation(hit)[: nexp - 2]})
-        pairs = []
-        for e in experts:
-            seg = sp[offsets[e]:offsets[e + 1]]
-            pairs.extend(int(p) for p in (seg if len(seg) <= 256 else np.r_[seg[:128], seg[-128:]]))
-        pairs = np.array(pairs)
-        emap = {e: i for i, e in enumerate(experts)}
-        sub = np.vectorize(lambda v: emap.get(int(v), -1))(ids).astype(np.int32)
-        ex_t = torch.tensor(experts, device="cuda")
-        if wl.kind == "moe_fp8":
-            x, sx = codes(inp["x"]), inp["sx"].cpu().numpy()
-            w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
-            fn = lambda: G.moe_w13_fp8(x, sx, w, sw, sub, pairs=pairs)  # noqa: E731
-            per_e = wl.N * wl.K
-        elif wl.kind == "moe_fp8_w2":
-            h, sh = codes(inp["h"]), inp["sh"].cpu().numpy()
-            w, sw = codes(inp["w"][ex_t]), inp["sw"][ex_t].cpu().numpy()
-            fn = lambda: G.moe_w2_fp8(h, sh, w, sw, sub, pairs=pairs)  # noqa: E731
-            per_e = wl.N * wl.K
-        else:
-            x = bits16(inp["x"])
-            w, ws = inp["w"][ex_t].cpu().numpy(), bits16(inp["ws"][ex_t])
-            fn = lambda: G.moe_w13_w4a16(x, w, ws, sub, pairs=pairs)  # noqa: E731
-            per_e = wl.N * wl.K // 2
-        s_flops = 2 * len(pairs) * wl.N * wl.K
-        s_bytes = len(experts) * per_e + len(pairs) * (wl.K + wl.N)
-        sample = f"{len(pairs)} routed rows of {len(experts)} experts (largest + smallest segment + random)"
-        got = got_all[pairs]
-    times = []
-    ref = fn()
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 100):
-        t0 = time.perf_counter()
-        ref = fn()
-        times.append(time.perf_counter() - t0)
+        x = bits16(inp["x"])
+        w, ws = inp["w"][ex_t].cpu().numpy(), bits16(inp["ws"][ex_t])
+        fo = lambda: G.moe_w13_w4a16(x, w, ws, sub, pairs=pairs)  # noqa: E731
+        ft = lambda: TC.moe_w13_w4a16(x, w, ws, sub, pairs)  # noqa: E731
+        per_e = wl.N * wl.K // 2
+    return (fo, ft, got_all[pairs], 2 * len(pairs) * wl.N * wl.K, len(experts) * per_e + len(pairs) * (wl.K + wl.N),
+            f"{len(pairs)} routed rows of {len(experts)} experts (largest + smallest segment + random)", False)
+
+
+def oracle_check(wl, runner) -> dict:
+    """The GPU result on the bounded sample against the numpy oracle (one run)."""
+    import numpy as np
+    from oracle import metrics as MT
+    fo, _, got, _, _, desc, exact = _sample(wl, runner)
+    ref = fo()
+    if exact:
+        ok = bool(np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1]))
+        return {"sample": desc, "max_rel_err": 0.0 if ok else float("inf"), "non_finite": 0, "correct": ok,
+                "bit_exact": ok}
+    err, nbad = MT.fp8_rel_err(got, ref)
+    return {"sample": desc, "max_rel_err": err, "non_finite": nbad, "correct": bool(nbad == 0 and err < 1e-2)}
+
+
+def cpu_baseline(wl, runner, budget_s: float = 12.0) -> dict:
+    """Check the GPU output against the numpy oracle on a bounded sample, then
+    time the PyTorch-CPU fp32 dequantize-then-matmul path (oracle.torch_cpu) on
+    the same sample with torch.set_num_threads(physical cores, capped by
+    OMP_NUM_THREADS): one warmup, then the median of at least 3 runs, repeated
+    up to ~budget_s seconds.  Throughput = the sample's FLOPs (or algorithmic
+    bytes) over the median run time.
+    """
+    import torch
+    check = oracle_check(wl, runner)
+    _, ft, _, s_flops, s_bytes, desc, _ = _sample(wl, runner)
+    thr = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(thr["threads"])
+    try:
+        ft()
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 100):
+            t0 = time.perf_counter()
+            ft()
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
     med = statistics.median(times)
-    if check is not None:
-        ok = check(ref)
-        err, nbad = (0.0 if ok else float("inf")), 0
-    else:
-        err, nbad = MT.fp8_rel_err(got, ref)
     unit, bound = unit_of(wl)
     value = s_flops / med / 1e12 if bound == "mfma" else s_bytes / med / 1e9
-    return {"value": round(value, 6), "unit": unit, "cores": _blas_threads(), "kind": "port",
-            "sample": f"{sample}; numpy fp32 oracle, median of {len(times)} runs ({med:.2f} s each)",
-            "tflops": round(s_flops / med / 1e12, 6), "max_rel_err": err, "non_finite": nbad,
-            "correct": bool(nbad == 0 and err < 1e-2)}
+    log(f"[bench] cpu baseline {wl.key}: {thr['threads']} torch threads (physical cores "
+        f"{thr['physical_cores']}, os.cpu_count() {thr['os_cpu_count']}), median {med:.3f} s of {len(times)} runs")
+    return {"value": round(value, 6), "unit": unit, "cores": thr["threads"], "kind": "port",
+            "sample": f"{desc}; PyTorch-CPU fp32 dequantize-then-matmul (oracle/torch_cpu.py), "
+                      f"median of {len(times)} runs ({med:.3f} s each)",
+            "physical_cores": thr["physical_cores"], "os_cpu_count": thr["os_cpu_count"],
+            "tflops": round(s_flops / med / 1e12, 6), "max_rel_err": check["max_rel_err"],
+            "non_finite": check["non_finite"], "correct": check["correct"], "oracle_check": check["sample"]}
 
 
 # ---------------------------------------------------------------------------- modes
@@ -405,16 +454,24 @@ def driver_mode(args) -> int:
     roof.update(timing)
     cpu = None if args.no_cpu_baseline else cpu_baseline(wl, runner, args.cpu_budget)
     also = []
+    correct_all = True
     for key in args.also:
         w2 = W.WORKLOADS[key]
         r2 = Runner(w2)
         m2, k2, t2 = time_steps(r2, max(10, args.steps), 3)
         u2, _ = unit_of(w2)
         rf = roofline_of(w2, r2, k2)
+        chk = oracle_check(w2, r2)
         also.append({"workload": key, "ms_per_step": round(m2, 5), "kernel_us": rf["kernel_us"],
-                     "achieved": rf["achieved"], "unit": u2, "frac": rf["frac"], "bound": rf["bound"], **t2})
+                     "achieved": rf["achieved"], "unit": u2, "frac": rf["frac"],
+                     "frac_attainable": rf["frac_attainable"], "bound": rf["bound"],
+                     **({"frac_bf16_peak": rf["frac_bf16_peak"]} if "frac_bf16_peak" in rf else {}),
+                     "oracle_check": chk, **t2})
+        correct_all = correct_all and chk["correct"]
         del r2
     correct = True if cpu is None else cpu["correct"]
+    if not correct_all:
+        log("[bench] an `also` workload failed its oracle check (see its oracle_check)")
     line = {
         "metric": METRIC, "value": round(value, 3) if correct else 0.0, "unit": unit, "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
@@ -482,6 +539,7 @@ def kernel_result_mode(args) -> int:
         ref[key] = round(cpu["tflops"], 6)
         rf = roofline_of(wl, runner, med)
         roof[key] = {"us": round(med * 1e3, 2), "gbps": round(runner.bytes / (med * 1e-3) / 1e9, 1),
+                     "flush": "write+read (not the reference protocol)" if args.flush_read else "write (reference)",
                      "tflops": round(tflops, 2), "bound": rf["bound"], "frac": rf["frac"],
                      "valid": cpu["correct"], "max_rel_err": cpu["max_rel_err"], "cpu_cores": cpu["cores"]}
         log(f"[kernel-result] {key}: {med * 1e3:.1f} us, {tflops:.2f} TFLOPS, "
@@ -509,8 +567,10 @@ def main(argv=None) -> int:
     ap.add_argument("--iters", type=int, default=300)
     ap.add_argument("--warmup-s", type=float, default=2.0)
     ap.add_argument("--flush-mb", type=int, default=512)
-    ap.add_argument("--flush-read", type=int, default=1,
-                    help="after the flush write, read a second buffer of the same size (1) or not (0)")
+    ap.add_argument("--flush-read", type=int, default=0,
+                    help="0 (default): the reference's write-only flush; 1: also read a second buffer of the same "
+                         "size after it, so the write-back of the zeroed lines ends before the timed launch "
+                         "(not the reference's protocol: those numbers are not comparable with its own)")
     ap.add_argument("--launch-only", type=int, default=0, metavar="N",
                     help="only launch the workload's GEMM N times (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",

@@ -45,30 +45,27 @@ static int cu_count() {
 // kernel), else the launch status.  KS = K-steps per wave = K / 128 / NW.
 template <int F, int EPI, int RB, int D, int NW = 8>
 static int try_stream(const SkinnyArgs& a_in, int dense_tiles, int max_tiles, hipStream_t st) {
-  // A unit is RB 16-row blocks (SiLU: one gate and one up block, RB = 2), so
-  // the unit count per token tile follows from RB here rather than from the
-  // caller (whose units_n sizes the per-unit fallback kernel).
-  const int unit_rows = EPI == kSilu ? 16 : 16 * RB;
-  const int out_rows = EPI == kSilu ? a_in.N / 2 : a_in.N;
-  if (out_rows % unit_rows != 0) return 1;
-  SkinnyArgs a = a_in;
-  a.units_n = out_rows / unit_rows;
+  // The unit count, K-steps per wave and tile-table span come from the
+  // host-only plan (stream_plan.hpp), which the CPU tests check over every
+  // configuration instantiated here: a unit is RB 16-row blocks (SiLU: one
+  // gate and one up block), counted from RB itself, not from the caller
+  // (whose units_n sizes the per-unit fallback kernel).
+  static_assert(EPI != kSilu || RB == 2, "SiLU units pair one gate and one up block");
+  const bool grouped = a_in.tiles != nullptr;
   // bf16 dense split-K: each work item covers K / nsplit (see stream_gemm_kernel)
-  const int nsplit = (F == kBF16 && a.tiles == nullptr && a.partial != nullptr) ? a.ksplit : 1;
-  if (nsplit < 1) return 1;
-  const int nkb = (a.K >> 7) / nsplit;
-  if ((a.K >> 7) % (NW * nsplit) != 0) return 1;
-  // INT4 unit scales are copied as 16-byte chunks of the scale rows.
-  if (F == kINT4 && ((reinterpret_cast<uintptr_t>(a.w_scale) & 15) != 0 || a.K % 256 != 0)) return 1;
+  const int nsplit = (F == kBF16 && !grouped && a_in.partial != nullptr) ? a_in.ksplit : 1;
   const int grid = cu_count();
-  // A work-group's tile table must fit its LDS copy.
-  const int tiles = a.tiles ? max_tiles : dense_tiles;
-  const long per = ((long)tiles * a.units_n + grid - 1) / grid;
-  if (a.tiles && per / a.units_n + 2 > kStreamMaxTiles) return 1;
+  const StreamPlan plan = stream_plan(EPI == kSilu, RB, NW, a_in.N, a_in.K, grouped ? max_tiles : dense_tiles,
+                                      grouped, nsplit, grid);
+  if (!plan.ok) return 1;
+  // INT4 unit scales are copied as 16-byte chunks of the scale rows.
+  if (F == kINT4 && ((reinterpret_cast<uintptr_t>(a_in.w_scale) & 15) != 0 || a_in.K % 256 != 0)) return 1;
+  SkinnyArgs a = a_in;
+  a.units_n = plan.units_n;
   // INT4 keeps at most one unit of scales ahead: ring depth <= KS.
   constexpr int D2 = (F == kINT4 && D > 2) ? 2 : D;
   constexpr int D4 = (F == kINT4 && D > 4) ? 4 : D;
-  switch (nkb / NW) {
+  switch (plan.ks) {
     case 2: return launch_stream<F, EPI, RB, NW, 2, D2>(a, dense_tiles, grid, st);
     case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, dense_tiles, grid, st);
     case 7: return launch_stream<F, EPI, RB, NW, 7, D>(a, dense_tiles, grid, st);

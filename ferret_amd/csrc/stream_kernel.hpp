@@ -26,6 +26,7 @@
 // weights).
 #pragma once
 #include "skinny_kernel.hpp"
+#include "stream_plan.hpp"
 
 namespace ferret {
 
@@ -46,8 +47,6 @@ struct StreamFmt<kINT4> {
   static constexpr int kRowB = 64;
   static constexpr int kInstr = 1;
 };
-
-constexpr int kStreamMaxTiles = 64;  // token tiles one work-group may touch (tile table in LDS)
 
 template <int F, int RB, int NW, int KS, int D>
 struct StreamCfg {

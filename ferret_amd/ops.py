@@ -33,6 +33,24 @@ def _dev(t: torch.Tensor, name: str, dtype=None, ndim=None) -> int:
     return t.data_ptr()
 
 
+def _out(t: torch.Tensor, name: str, shape: tuple, dtype, device) -> int:
+    """Validate a caller-supplied output (or secondary input) tensor: exact shape,
+    dtype, contiguity and the same device as the inputs; a smaller buffer would
+    let the kernel write past its allocation."""
+    ptr = _dev(t, name, dtype)
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, the inputs on {device}")
+    return ptr
+
+
+def _same_device(*ts) -> None:
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) > 1:
+        raise ValueError(f"all tensors must be on one device, got {sorted(str(d) for d in devs)}")
+
+
 def linear_workspace_bytes(M: int, N: int, K: int) -> int:
     """Split-K workspace ferret_linear_bf16 can use for this shape (0: none)."""
     return int(_lib.load().ferret_workspace_bytes(0, M, N, K, 0))
@@ -46,17 +64,19 @@ def linear_bf16(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor | None 
     `workspace`, or from torch's caching allocator when none (or a too small
     one) is passed.
     """
+    _dev(x, "x", torch.bfloat16, 2)
+    _dev(w, "w", torch.bfloat16, 2)
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    _same_device(x, w, residual, out, workspace)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _out(out, "out", (M, N), torch.bfloat16, x.device)
     rp = 0
     if residual is not None:
-        if tuple(residual.shape) != (M, N):
-            raise ValueError("residual must be [M, N]")
-        rp = _dev(residual, "residual", torch.bfloat16)
+        rp = _out(residual, "residual", (M, N), torch.bfloat16, x.device)
     need = linear_workspace_bytes(M, N, K) if K % 128 == 0 and N % 16 == 0 else 0
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
@@ -90,14 +110,18 @@ def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: 
     taken from torch's caching allocator).  mma="e4m3" opts the tiled (M > 16)
     kernels into the FP8 MFMA (FERRET_FP8_MMA_E4M3: faster, less precise).
     """
+    _dev(a, "a", (FP8, torch.uint8), 2)
+    _dev(b, "b", (FP8, torch.uint8), 2)
     M, K = a.shape
     N = b.shape[0]
     if b.shape[1] != K:
         raise ValueError("b must be [N, K]")
     if tuple(sa.shape) != (M, K // 128) or tuple(sb.shape) != ((N + 127) // 128, K // 128):
         raise ValueError(f"scale shapes must be sa [M, K/128], sb [ceil(N/128), K/128]; got {tuple(sa.shape)}, {tuple(sb.shape)}")
+    _same_device(a, sa, b, sb, out, workspace)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _out(out, "out", (M, N), torch.bfloat16, a.device)
     need = fp8_workspace_bytes(M, N, K)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
@@ -182,9 +206,11 @@ def moe_w13_fp8(x: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, sw: torch.Te
         raise ValueError("shape mismatch between x, w and routing")
     if tuple(sx.shape) != (T, K // 128) or tuple(sw.shape) != (E, N // 128, K // 128):
         raise ValueError("scale shapes must be sx [T, K/128], sw [E, N/128, K/128]")
+    _same_device(x, sx, w, sw, routing.sorted_pair, routing.tiles, out)
     P = T * routing.topk
     if out is None:
         out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
+    _out(out, "out", (P, N // 2), torch.bfloat16, x.device)
     rc = _lib.load().ferret_moe_w13_fp8_ex(
         _dev(x, "x", (FP8, torch.uint8), 2), _dev(sx, "sx", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
         _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
@@ -203,9 +229,11 @@ def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: 
         raise ValueError("shape mismatch between x, wq and routing")
     if tuple(ws.shape) != (E, N, K // 32):
         raise ValueError("ws must be [E, N, K/32] bf16")
+    _same_device(x, wq, ws, routing.sorted_pair, routing.tiles, out)
     P = T * routing.topk
     if out is None:
         out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
+    _out(out, "out", (P, N // 2), torch.bfloat16, x.device)
     rc = _lib.load().ferret_moe_w13_w4a16(
         _dev(x, "x", torch.bfloat16, 2), _dev(wq, "wq", torch.int32, 3), _dev(ws, "ws", torch.bfloat16, 3),
         routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(), routing.ntiles.data_ptr(), routing.max_tiles,
@@ -216,13 +244,17 @@ def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: 
 
 def quant_act_e4m3(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tensor | None = None):
     """bf16 x [M, K] -> (e4m3 q [M, K], fp32 scale [M, K/128]) by the 1x128 absmax/448 rule."""
+    _dev(x, "x", torch.bfloat16, 2)
     M, K = x.shape
+    _same_device(x, q, scale)
     if q is None:
         q = torch.empty((M, K), dtype=FP8, device=x.device)
     if scale is None:
         scale = torch.empty((M, K // 128), dtype=torch.float32, device=x.device)
-    rc = _lib.load().ferret_quant_act_e4m3(_dev(x, "x", torch.bfloat16, 2), _dev(q, "q", (FP8, torch.uint8), 2),
-                                           _dev(scale, "scale", torch.float32, 2), M, K, _stream())
+    rc = _lib.load().ferret_quant_act_e4m3(_dev(x, "x", torch.bfloat16, 2),
+                                           _out(q, "q", (M, K), (FP8, torch.uint8), x.device),
+                                           _out(scale, "scale", (M, K // 128), torch.float32, x.device), M, K,
+                                           _stream())
     _lib.check("ferret_quant_act_e4m3", rc)
     return q, scale
 
@@ -236,8 +268,10 @@ def moe_w2_fp8(h: torch.Tensor, sh: torch.Tensor, w: torch.Tensor, sw: torch.Ten
         raise ValueError("shape mismatch between h, w and routing")
     if tuple(sh.shape) != (P, K // 128) or tuple(sw.shape) != (E, N // 128, K // 128):
         raise ValueError("scale shapes must be sh [P, K/128], sw [E, N/128, K/128]")
+    _same_device(h, sh, w, sw, routing.sorted_pair, routing.tiles, out)
     if out is None:
         out = torch.empty((P, N), dtype=torch.bfloat16, device=h.device)
+    _out(out, "out", (P, N), torch.bfloat16, h.device)
     rc = _lib.load().ferret_moe_w2_fp8_ex(
         _dev(h, "h", (FP8, torch.uint8), 2), _dev(sh, "sh", torch.float32, 2), _dev(w, "w", (FP8, torch.uint8), 3),
         _dev(sw, "sw", torch.float32, 3), routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(),
@@ -253,8 +287,10 @@ def moe_combine(o: torch.Tensor, weights: torch.Tensor, out: torch.Tensor | None
     P, N = o.shape
     if P != T * topk:
         raise ValueError("o must hold T*topk rows in pair order")
+    _same_device(o, weights, out)
     if out is None:
         out = torch.empty((T, N), dtype=torch.bfloat16, device=o.device)
+    _out(out, "out", (T, N), torch.bfloat16, o.device)
     rc = _lib.load().ferret_moe_combine(_dev(o, "o", torch.bfloat16, 2), _dev(weights, "weights", torch.float32, 2),
                                         T, topk, N, _dev(out, "out", torch.bfloat16, 2), _stream())
     _lib.check("ferret_moe_combine", rc)

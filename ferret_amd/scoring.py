@@ -3,7 +3,8 @@
 Mirrors the reference's scoring surface so that bench output from this build is
 parsed and scored unchanged:
 
-* ``load_task_spec``      — task_spec.py:104-269 (required keys, validation errors)
+* ``load_task_spec``      — loads the task.yaml schema of tasks/template.yaml (this
+  module's own validator; the reference's is task_spec.py:104-269)
 * ``parse_kernel_output`` — task_spec.py:283-328 (KERNEL_RESULT JSON line, then
   the legacy "Q_LEN=N: x TFLOPS" and "TFLOPS: Q1=..." forms)
 * ``parse_reference_output`` — task_spec.py:331-356 (KERNEL_RESULT_REFERENCE)
@@ -64,88 +65,131 @@ class TaskSpec:
     result_keys: list[str] = field(default_factory=list)
 
 
-def _require(cond: bool, msg: str) -> None:
-    if not cond:
-        raise ValueError(msg)
+# ---------------------------------------------------------------------------- task.yaml
+
+# The task.yaml schema this loader accepts (the keys the reference's task
+# files use, tasks/template.yaml): top-level keys with their YAML kinds, the
+# required sub-keys of the two nested mappings, and per-config keys with
+# defaults.  Everything is checked and every problem is reported in one error.
+_TOP_LEVEL = {"name": str, "gpu": str, "arch": str, "precision": str, "problem": dict, "baseline": dict,
+              "configs": list}
+_NESTED = {"problem": ("description", "shapes"), "baseline": ("source",)}
+_CONFIG_DEFAULTS = {"target_ratio": 0.95, "weight": 1.0}
+_OPTIONAL_LISTS = ("constraints", "hints", "references")
 
 
-def _number(value, what: str) -> float:
+class _Problems:
+    """Collects schema violations; `raise_if_any` turns them into one ValueError."""
+
+    def __init__(self, where: str):
+        self.where = where
+        self.items: list[str] = []
+
+    def add(self, msg: str) -> None:
+        self.items.append(msg)
+
+    def raise_if_any(self) -> None:
+        if self.items:
+            raise ValueError(f"{self.where}: " + "; ".join(self.items))
+
+
+def _as_float(value, problems: _Problems, label: str, default: float) -> float:
     try:
         return float(value)
-    except (TypeError, ValueError) as exc:
-        raise ValueError(f"{what} must be a number") from exc
+    except (TypeError, ValueError):
+        problems.add(f"{label} is not a number ({value!r})")
+        return default
+
+
+def _load_configs(raw, problems: _Problems) -> list[ConfigEntry]:
+    configs: list[ConfigEntry] = []
+    seen: set[str] = set()
+    for idx, entry in enumerate(raw):
+        if not isinstance(entry, dict) or "name" not in entry or not isinstance(entry.get("args"), dict):
+            problems.add(f"configs entry #{idx} needs a name and an args mapping")
+            continue
+        name = str(entry["name"])
+        if name in seen:
+            problems.add(f"config name {name!r} appears twice")
+        seen.add(name)
+        vals = {k: _as_float(entry.get(k, d), problems, f"{name}.{k}", d) for k, d in _CONFIG_DEFAULTS.items()}
+        if vals["target_ratio"] <= 0:
+            problems.add(f"{name}.target_ratio has to be positive")
+        if vals["weight"] < 0:
+            problems.add(f"{name}.weight cannot be negative")
+        configs.append(ConfigEntry(name, entry["args"], vals["target_ratio"], vals["weight"]))
+    return configs
 
 
 def load_task_spec(path: str | Path) -> TaskSpec:
-    """Load and validate a task.yaml; raise ValueError with a clear message on bad input."""
+    """Parse a task.yaml into a TaskSpec; a file that breaks the schema above
+    raises one ValueError naming every problem found."""
     path = Path(path)
-    _require(path.exists(), f"task spec not found: {path}")
+    if not path.is_file():
+        raise ValueError(f"{path}: no such task file")
     try:
         data = yaml.safe_load(path.read_text())
     except yaml.YAMLError as exc:
-        raise ValueError(f"task spec is not valid YAML: {exc}") from exc
-    _require(isinstance(data, dict), f"task spec must be a YAML mapping, got {type(data).__name__}")
-    for key in ("name", "gpu", "arch", "precision", "problem", "baseline", "configs"):
-        _require(key in data, f"task spec missing required field: {key}")
+        raise ValueError(f"{path}: unreadable YAML ({exc})") from exc
+    problems = _Problems(str(path))
+    if not isinstance(data, dict):
+        problems.add(f"top level is a {type(data).__name__}, not a mapping")
+        problems.raise_if_any()
+
+    for key, kind in _TOP_LEVEL.items():
+        if key not in data:
+            problems.add(f"'{key}' is absent")
+        elif kind is not str and not isinstance(data[key], kind):
+            problems.add(f"'{key}' should be a {kind.__name__}")
+    for key, subkeys in _NESTED.items():
+        if isinstance(data.get(key), dict):
+            for sub in subkeys:
+                if sub not in data[key]:
+                    problems.add(f"'{key}.{sub}' is absent")
+    if isinstance(data.get("problem"), dict) and "shapes" in data["problem"] \
+            and not isinstance(data["problem"]["shapes"], dict):
+        problems.add("'problem.shapes' should be a mapping")
+    problems.raise_if_any()
+
+    if not data["configs"]:
+        problems.add("'configs' is empty")
+    configs = _load_configs(data["configs"], problems)
+    names = [c.name for c in configs]
+
+    scoring = str(data.get("scoring", SCORING_POLICIES[0]))
+    focus = str(data.get("focus_config", ""))
+    if scoring not in SCORING_POLICIES:
+        problems.add(f"scoring {scoring!r} is not one of {', '.join(SCORING_POLICIES)}")
+    elif scoring == "focus" and focus not in names:
+        problems.add(f"focus_config {focus!r} has to name one of the configs {names}")
+    elif scoring == "weighted_avg" and not any(c.weight > 0 for c in configs):
+        problems.add("weighted_avg scoring needs a config with a positive weight")
+
+    gate = data.get("stage_gate") or {}
+    output = data.get("output") or {}
+    if not isinstance(gate, dict):
+        problems.add("'stage_gate' should be a mapping")
+        gate = {}
+    if not isinstance(output, dict):
+        problems.add("'output' should be a mapping")
+        output = {}
+    gate_ratio = _as_float(gate.get("ratio", 0.9), problems, "stage_gate.ratio", 0.9)
+    if gate_ratio <= 0:
+        problems.add("stage_gate.ratio has to be positive")
+    lists = {key: list(data.get(key) or []) for key in _OPTIONAL_LISTS}
+    for key, vals in lists.items():
+        if not all(isinstance(v, str) for v in vals):
+            problems.add(f"'{key}' should list strings")
+    problems.raise_if_any()
 
     problem = data["problem"]
-    _require(isinstance(problem, dict), "task spec.problem must be a mapping")
-    _require("description" in problem, "task spec.problem missing required field: description")
-    _require("shapes" in problem, "task spec.problem missing required field: shapes")
-    _require(isinstance(problem["shapes"], dict), "task spec.problem.shapes must be a mapping")
-    baseline = data["baseline"]
-    _require(isinstance(baseline, dict), "task spec.baseline must be a mapping")
-    _require("source" in baseline, "task spec.baseline missing required field: source")
-
-    raw_configs = data["configs"]
-    _require(isinstance(raw_configs, list) and raw_configs, "task spec.configs must be a non-empty list")
-    configs: list[ConfigEntry] = []
-    names: set[str] = set()
-    for i, c in enumerate(raw_configs):
-        _require(isinstance(c, dict), f"config[{i}] must be a mapping")
-        for req in ("name", "args"):
-            _require(req in c, f"config[{i}] missing required field: {req}")
-        name = str(c["name"])
-        _require(name not in names, f"duplicate config name: {name}")
-        names.add(name)
-        _require(isinstance(c["args"], dict), f"config[{i}] ({name}).args must be a mapping")
-        target = _number(c.get("target_ratio", 0.95), f"config[{i}] ({name}).target_ratio")
-        weight = _number(c.get("weight", 1.0), f"config[{i}] ({name}).weight")
-        _require(target > 0, f"config[{i}] ({name}).target_ratio must be > 0")
-        _require(weight >= 0, f"config[{i}] ({name}).weight must be >= 0")
-        configs.append(ConfigEntry(name, c["args"], target, weight))
-
-    scoring = str(data.get("scoring", "min_ratio"))
-    _require(scoring in SCORING_POLICIES,
-             f"invalid scoring policy: {scoring!r}. Must be one of {SCORING_POLICIES}")
-    focus = str(data.get("focus_config", ""))
-    if scoring == "focus":
-        _require(bool(focus), "scoring=focus requires focus_config to be set")
-        _require(focus in names, f"focus_config {focus!r} not in configs list (available: {[c.name for c in configs]})")
-    if scoring == "weighted_avg":
-        _require(sum(c.weight for c in configs) > 0,
-                 "scoring=weighted_avg requires at least one config with weight > 0")
-
-    gate = data.get("stage_gate", {}) or {}
-    _require(isinstance(gate, dict), "task spec.stage_gate must be a mapping")
-    gate_ratio = _number(gate.get("ratio", 0.9), "task spec.stage_gate.ratio")
-    _require(gate_ratio > 0, "task spec.stage_gate.ratio must be > 0")
-
-    output = data.get("output", {}) or {}
-    _require(isinstance(output, dict), "task spec.output must be a mapping")
-    lists = {}
-    for key in ("constraints", "hints", "references"):
-        vals = list(data.get(key, []) or [])
-        _require(all(isinstance(v, str) for v in vals), f"task spec.{key} must be a list of strings")
-        lists[key] = vals
-
     return TaskSpec(
-        name=str(data["name"]), gpu=str(data["gpu"]), arch=str(data["arch"]),
-        precision=str(data["precision"]), description=str(problem["description"]),
-        shapes=dict(problem["shapes"]), baseline_source=str(baseline["source"]), configs=configs,
-        scoring=scoring, focus_config=focus, stage_gate=StageGate(gate_ratio, bool(gate.get("strict", False))),
-        constraints=lists["constraints"], hints=lists["hints"], references=lists["references"],
-        result_keys=list(output.get("result_keys", [c.name for c in configs])))
+        name=str(data["name"]), gpu=str(data["gpu"]), arch=str(data["arch"]), precision=str(data["precision"]),
+        description=str(problem["description"]), shapes=dict(problem["shapes"]),
+        baseline_source=str(data["baseline"]["source"]), configs=configs, scoring=scoring, focus_config=focus,
+        stage_gate=StageGate(gate_ratio, bool(gate.get("strict", False))), constraints=lists["constraints"],
+        hints=lists["hints"], references=lists["references"],
+        result_keys=list(output.get("result_keys", names)))
 
 
 def _json_numbers(text: str) -> dict[str, float] | None:

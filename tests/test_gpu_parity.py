@@ -112,6 +112,42 @@ def test_linear_bf16_rejects_bad_shapes(ops):
         ops.linear_bf16(x, w)
 
 
+def test_wrappers_reject_wrong_output_buffers(ops):
+    """A caller-supplied output (or q/scale) of the wrong shape is refused on the
+    host, before any launch could write past it."""
+    from ferret_amd import workloads as W
+    x = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.linear_bf16(x, w, out=torch.empty((4, 32), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="residual must have shape"):
+        ops.linear_bf16(x, w, residual=torch.empty((2, 64), dtype=torch.bfloat16, device="cuda"))
+    a, sa = W.quant_act_1x128(W.randn((32, 256), 1, "cuda"))
+    b, sb = W.quant_weight_128x128(W.randn((128, 256), 2, "cuda"))
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.fp8_gemm_blockscale(a, sa, b, sb, out=torch.empty((32, 64), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="q must have shape"):
+        ops.quant_act_e4m3(x, q=torch.empty((4, 128), dtype=torch.float8_e4m3fn, device="cuda"))
+    with pytest.raises(ValueError, match="scale must have shape"):
+        ops.quant_act_e4m3(x, scale=torch.empty((4, 1), dtype=torch.float32, device="cuda"))
+    ids = torch.zeros((4, 2), dtype=torch.int32, device="cuda")
+    rt = ops.moe_permute(ids, 4)
+    xq, sx = W.quant_act_1x128(W.randn((4, 256), 3, "cuda"))
+    wq = torch.zeros((4, 256, 256), dtype=torch.float8_e4m3fn, device="cuda")
+    sw = torch.ones((4, 2, 2), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.moe_w13_fp8(xq, sx, wq, sw, rt, out=torch.empty((8, 64), dtype=torch.bfloat16, device="cuda"))
+    h, sh = W.quant_act_1x128(W.randn((8, 256), 4, "cuda"))
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.moe_w2_fp8(h, sh, wq, sw, rt, out=torch.empty((8, 128), dtype=torch.bfloat16, device="cuda"))
+    o = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
+    wts = torch.ones((4, 2), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.moe_combine(o, wts, out=torch.empty((4, 32), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="one device"):
+        ops.moe_combine(o, wts.cpu())
+
+
 # ------------------------------------------------------------------ FP8 dense
 
 def _fp8_inputs(M, N, K, seed):
@@ -340,7 +376,9 @@ _ATTN_TP8 = [f"dsv3_{p}_M{m}" for m in (1, 16, 512, 1024, 2048, 4096, 8192)
              for p in ("q_b_proj", "kv_b_proj", "o_proj")]
 
 
-@pytest.mark.parametrize("key", ["qwen3_gateup_M16", "dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096"]
+@pytest.mark.parametrize("key", ["qwen3_gateup_M16", "dsv3_fp8_M16", "dsv3_fp8_M128", "dsv3_fp8_M4096",
+                                 "qwen3_lmhead_M16", "qwen3_lmhead_M1", "qwen3_qkv_M16", "qwen3_down_M16",
+                                 "qwen3_o_M1"]
                          + _ATTN_TP8)
 def test_dense_full_size(ops, key):
     from ferret_amd import workloads as W
@@ -348,10 +386,11 @@ def test_dense_full_size(ops, key):
     _say(f"full-size {key}")
     inp = W.make_inputs(wl, "cuda")
     if wl.kind == "linear_bf16":
-        y = ops.linear_bf16(inp["x"], inp["w"])
-        y2 = ops.linear_bf16(inp["x"], inp["w"])
+        r = inp.get("r")
+        y = ops.linear_bf16(inp["x"], inp["w"], residual=r)
+        y2 = ops.linear_bf16(inp["x"], inp["w"], residual=r)
         torch.cuda.synchronize()
-        ref = G.linear_bf16(bits16(inp["x"]), bits16(inp["w"]))
+        ref = G.linear_bf16(bits16(inp["x"]), bits16(inp["w"]), bits16(r) if r is not None else None)
         assert_gemm_close(bf16_out(y), ref, key)
     else:
         y = ops.fp8_gemm_blockscale(inp["a"], inp["sa"], inp["b"], inp["sb"])
@@ -365,7 +404,7 @@ def test_dense_full_size(ops, key):
 
 
 @pytest.mark.parametrize("key", ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill",
-                                 "kimi_w4a16_w13_T8_tp8"]
+                                 "kimi_w4a16_w13_T8_tp8", "dsv3_moe_w2_decode", "dsv3_moe_w2_prefill"]
                          + [f"dsv3_ep8_{p}_M{m}" for m in (1, 16, 64, 512) for p in ("gate_up", "down")])
 def test_moe_full_size(ops, key):
     from ferret_amd import workloads as W

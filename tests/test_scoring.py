@@ -92,14 +92,17 @@ focus_config: b
 
 
 def test_validation_errors(tmp_path):
-    with pytest.raises(ValueError, match="missing required field: configs"):
+    with pytest.raises(ValueError, match="'configs' is absent"):
         _spec(tmp_path, BASE)
-    with pytest.raises(ValueError, match="duplicate config name"):
+    with pytest.raises(ValueError, match="appears twice"):
         _spec(tmp_path, BASE + "configs:\n  - {name: a, args: {}}\n  - {name: a, args: {}}\n")
-    with pytest.raises(ValueError, match="invalid scoring policy"):
+    with pytest.raises(ValueError, match="scoring 'best' is not one of"):
         _spec(tmp_path, BASE + "configs:\n  - {name: a, args: {}}\nscoring: best\n")
     with pytest.raises(ValueError, match="focus_config"):
         _spec(tmp_path, BASE + "configs:\n  - {name: a, args: {}}\nscoring: focus\nfocus_config: z\n")
+    # every problem of one file is reported together
+    with pytest.raises(ValueError, match="target_ratio has to be positive.*weight cannot be negative"):
+        _spec(tmp_path, BASE + "configs:\n  - {name: a, args: {}, target_ratio: 0, weight: -1}\n")
 
 
 def test_mi355x_task_files_load_and_match_bench_families():
