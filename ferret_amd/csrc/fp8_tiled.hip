@@ -15,8 +15,9 @@
 // Work-group (large M): 512 threads = 8 waves (4 along weight rows x 2 along
 // tokens, two per SIMD so one wave's conversions overlap the other's MFMAs),
 // tile 256 weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
-// Small M (<= 256) with a workspace: 128 x 128 tiles (4 waves) over K ranges
-// (split-K), fp32 partials summed in split order by a reduce kernel.
+// Small M (<= 256) with a workspace: 128 x 128 tiles of 8 waves (64 weight
+// rows x 32 tokens each, again two per SIMD) over K ranges (split-K), fp32
+// partials summed in split order by a reduce kernel.
 // Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
 // staging) through a 3-stage ring; every load instruction reads complete
 // 128-byte lines; LDS rows of 128 B have their 16-byte chunk index
@@ -38,14 +39,18 @@ namespace ferret {
 constexpr int TB_K = 128;  // K per step (one scale block)
 constexpr int TB_M = 128;  // tokens per work-group (two token waves carry the 128 activation scales)
 
-// Tile geometry: WN waves along the weight rows (64 rows each) x 2 waves along
-// the tokens (64 each).  WN = 4: 256 x 128 tile, 8 waves (two per SIMD) for
-// large M; WN = 2: 128 x 128 tile, 4 waves, used with split-K for small M.
-template <int WN>
+// Tile geometry: WN waves along the weight rows (64 rows each) x TW waves along
+// the 128 tokens (128 / TW each).  WN = 4, TW = 2: 256 x 128 tile, 8 waves (two
+// per SIMD) for large M; WN = 2, TW = 4: 128 x 128 tile, 8 waves of 64 x 32,
+// used with split-K for small M.
+template <int WN, int TW = 2>
 struct TileCfg {
   static constexpr int kWN = WN;
-  static constexpr int kWaves = WN * 2;
+  static constexpr int kTW = TW;
+  static constexpr int kWaves = WN * TW;
   static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kTokW = TB_M / TW;                  // tokens per wave
+  static constexpr int kMI = kTokW / 16;                   // 16-token sub-tiles per wave
   static constexpr int kN = 64 * WN;                       // weight rows per work-group
   static constexpr int kWBytes = kN * TB_K;                // weight rows (e4m3) of a stage
   static constexpr int kABytes = TB_M * TB_K;              // token rows (e4m3) of a stage
@@ -57,7 +62,8 @@ struct TileCfg {
   static constexpr int kLds = kNS * kStage;                // WN=4: 145.5 KB of the 160 KB LDS
   static_assert((kWBytes + kABytes) % (1024 * kWaves) == 0, "stage loads split evenly over the waves");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(kThreads == 128 * WN, "fp8_tiled_kernel launch bounds");
+  static_assert(TW == 2 || TW == 4, "token halves pair up on the SIMDs");
+  static_assert(kThreads == 64 * WN * TW, "fp8_tiled_kernel launch bounds");
 };
 
 struct TiledArgs {
@@ -103,10 +109,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // FP8 datapath aligns the products of a dot-product group to a narrow window,
 // which costs about 1e-5 of max|C| at K = 7168 (an opt-in instance, see
 // FERRET_FP8_MMA_E4M3).
-template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8 = false>
-__global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8 = false, int TW = 2>
+__global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
   static_assert(!SILU || GROUPED, "the SiLU epilogue is the grouped w13 GEMM's");
-  using C = TileCfg<WN>;
+  static_assert(TW == 2 || SPLIT, "the bf16 and SiLU epilogues take 64-token waves");
+  using C = TileCfg<WN, TW>;
+  constexpr int MIX = C::kMI, TOKW = C::kTokW;
   constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
   constexpr int TB_LD_PER_WAVE = C::kLdPerWave, TB_SA_OFF = C::kSaOff, TB_STAGE = C::kStage;
   constexpr int TB_NS = C::kNS;
@@ -116,7 +124,10 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS bases in SGPRs
   const int wn = wave % TB_WN;  // weight-row block of the tile
-  const int wm = wave / TB_WN;  // token half of the tile
+  const int wm = wave / TB_WN;  // token block of the tile (TOKW tokens)
+  // Token half: waves w and w + 4 share a SIMD (work-group waves are dealt to
+  // the four SIMDs round-robin) and always sit in opposite halves.
+  const bool stag = wm >= TW / 2;
   const int r = lane & 15;
   const int g = lane >> 4;
 
@@ -246,9 +257,9 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni)
     wfrag_row[ni] = SILU ? (wn * 32 + (ni & 1) * 16 + (ni >> 1) * (TB_N / 2) + r) : (wn * 64 + ni * 16 + r);
-  int afrag_row[4];
+  int afrag_row[MIX];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) afrag_row[mi] = wm * 64 + mi * 16 + r;
+  for (int mi = 0; mi < MIX; ++mi) afrag_row[mi] = wm * TOKW + mi * 16 + r;
 
   // The wave's weight-scale rows (<= 128 K-steps) are loaded once into lanes
   // (lane l holds K-steps l and 64 + l) before any stage is in flight; each
@@ -262,27 +273,27 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   const float sbu_lo = SILU && lane < nkb ? sbp[(size_t)sb_up * nkb + lane] : 0.f;
   const float sbu_hi = SILU && 64 + lane < nkb ? sbp[(size_t)sb_up * nkb + 64 + lane] : 0.f;
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][MIX];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mi = 0; mi < MIX; ++mi) acc[ni][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Prologue: stages 0 .. NS-2 in flight (and stage NS-1 too from the
   // token-half-1 waves of the staggered loop, see below).
 #pragma unroll
   for (int s = 0; s < TB_NS - 1; ++s)
     if (s < nsteps) issue_stage(s);
-  if (wm == 1 && TB_NS - 1 < nsteps) issue_stage(TB_NS - 1);
+  if (stag && TB_NS - 1 < nsteps) issue_stage(TB_NS - 1);
 
   // One K-step is two phases: X (LDS fragment reads + e4m3 -> bf16 widening,
   // VALU only) and Y (the MFMAs + the scale folds).  Fragments widened by X
   // live in registers until Y.  Both take the number MI of 16-token sub-tiles
   // of this wave that hold tokens (a partial tile of a grouped GEMM skips the
   // empty ones; MI is uniform per wave).
-  bf16x8 abf[4][4], wbf[4][4];
-  i32x8 araw[4], wraw[4];  // F8: the raw e4m3 bytes of each fragment
-  float sa_v[4], sbg = 0.f, sbu = 0.f;
+  bf16x8 abf[MIX][4], wbf[4][4];
+  i32x8 araw[MIX], wraw[4];  // F8: the raw e4m3 bytes of each fragment
+  float sa_v[MIX], sbg = 0.f, sbu = 0.f;
   auto phase_x = [&](auto mic, int step) {
     constexpr int MI = decltype(mic)::value;
     const int kb = kb0 + step;
@@ -329,7 +340,7 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     // past the copy branches into Y, where they queue behind the same wave's
     // MFMAs instead of overlapping the partner wave's (8 % of the M = 4096
     // GEMM; the 4-wave tiles are faster unpinned).
-    if constexpr (WN == 4 && !F8) {
+    if constexpr (TB_WAVES == 8 && !F8) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -345,13 +356,13 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   // token half 1 above half 0 in either, so half 0 no longer races ahead and
   // idles at the barrier while half 1 widens its fragments alone.
   auto set_prio = [&](bool y) {
-    if constexpr (WN == 4) {
+    if constexpr (TB_WAVES == 8) {
       __builtin_amdgcn_sched_barrier(0);
       if (y) {
-        if (wm == 1) __builtin_amdgcn_s_setprio(3);
+        if (stag) __builtin_amdgcn_s_setprio(3);
         else __builtin_amdgcn_s_setprio(2);
       } else {
-        if (wm == 1) __builtin_amdgcn_s_setprio(1);
+        if (stag) __builtin_amdgcn_s_setprio(1);
         else __builtin_amdgcn_s_setprio(0);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -406,8 +417,9 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   };
   {
-    // Staggered halves: waves w and w + WN share a SIMD (work-group waves are
-    // dealt to the four SIMDs round-robin).  Between the barriers that open
+    // Staggered halves: waves w and w + 4 share a SIMD (work-group waves are
+    // dealt to the four SIMDs round-robin) and lie in opposite token halves
+    // (stag).  Between the barriers that open
     // K-steps s and s+1 the token-half-0 waves run X(s) Y(s) and the
     // token-half-1 waves Y(s-1) X(s), so one wave's MFMAs overlap its
     // partner's VALU widening; both halves pass the same nsteps + 1 barriers,
@@ -441,12 +453,12 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
       }
     };
     auto run = [&](auto mic) {
-      if (wm == 0) half0(mic);
+      if (!stag) half0(mic);
       else half1(mic);
     };
-    switch (FULL ? 4 : max(0, min(4, (nrows - wm * 64 + 15) / 16))) {
-      case 4: run(IntC<4>{}); break;
-      case 3: run(IntC<3>{}); break;
+    switch (FULL ? MIX : max(0, min(MIX, (nrows - wm * TOKW + 15) / 16))) {
+      case 4: if constexpr (MIX >= 4) run(IntC<4>{}); break;
+      case 3: if constexpr (MIX >= 3) run(IntC<3>{}); break;
       case 2: run(IntC<2>{}); break;
       case 1: run(IntC<1>{}); break;
       default: run(IntC<0>{}); break;
@@ -490,8 +502,8 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
     // silu(gate) * up, bf16, to the routed pair's row (staging these 64-B
     // rows through the LDS measured no faster).
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int tl = wm * 64 + mi * 16 + r;  // token row inside the tile
+    for (int mi = 0; mi < MIX; ++mi) {
+      const int tl = wm * TOKW + mi * 16 + r;  // token row inside the tile
       if (tl >= nrows) continue;
       const int pair = p.sorted_pair[row0 + tl];
       uint16_t* o = p.out + (size_t)pair * (N / 2) + nb * (TB_N / 2) + wn * 32;
@@ -506,8 +518,8 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
   } else {
     // split-K: fp32 partials, 16 B per lane.
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int tl = wm * 64 + mi * 16 + r;  // token row inside the tile
+    for (int mi = 0; mi < MIX; ++mi) {
+      const int tl = wm * TOKW + mi * 16 + r;  // token row inside the tile
       if (tl >= nrows || nb * TB_N + wn * 64 >= N) continue;
       float* o = p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64;
 #pragma unroll
@@ -520,34 +532,38 @@ __global__ __launch_bounds__(128 * WN) void fp8_tiled_kernel(TiledArgs p) {
 
 using namespace ferret;
 
-template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8>
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8, int TW>
 static int launch_tiled_one(const TiledArgs& p, dim3 grid, hipStream_t st) {
-  using C = TileCfg<WN>;
-  FERRET_HIP_CHECK((set_lds_limit_once<fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8>>(C::kLds)));
-  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8>), grid, dim3(C::kThreads), C::kLds, st,
-                     p);
+  using C = TileCfg<WN, TW>;
+  FERRET_HIP_CHECK((set_lds_limit_once<fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8, TW>>(C::kLds)));
+  hipLaunchKernelGGL((fp8_tiled_kernel<SILU, GROUPED, WN, SPLIT, FULL, F8, TW>), grid, dim3(C::kThreads), C::kLds,
+                     st, p);
   return (int)hipGetLastError();
 }
 
 // f8: the FP8-MFMA instance (FERRET_FP8_MMA_E4M3), else the exact bf16 one.
-template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL>
+template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, int TW = 2>
 static int launch_tiled(const TiledArgs& p, dim3 grid, hipStream_t st, bool f8) {
-  return f8 ? launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, true>(p, grid, st)
-            : launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, false>(p, grid, st);
+  return f8 ? launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, true, TW>(p, grid, st)
+            : launch_tiled_one<SILU, GROUPED, WN, SPLIT, FULL, false, TW>(p, grid, st);
 }
 
-// Split-K plan for small M: 128 x 128 tiles (4 waves) over K ranges, the
-// number of splits doubled until the grid covers the 256 CUs once (measured
-// on 128 x 4096 x 7168 against 64 x 128 and 256 x 128 tiles and 2 grids per
-// CU: 28 us vs 29-36 us).  Returns the number of splits (1 = no split-K).
-constexpr int SPLITK_WN = 2;         // 128 x 128 tiles (4 waves)
-constexpr int SPLITK_TARGET = 256;   // work-groups the split grid should reach
+// Split-K plan for small M: 128 x 128 tiles (8 waves) over K ranges, the
+// number of splits the largest power of two whose grid still fits the 256 CUs
+// in one round (one 97.5-KB work-group per CU): a grid of 448 at
+// 128 x 7168 x 2048 ran in two rounds, 26.5 us against 15.7 us with 224.
+// At 128 x 4096 x 7168 (256 work-groups) this beat 64 x 128 and 256 x 128
+// tiles and two work-groups per CU (28 us vs 29-36 us).  Returns the number
+// of splits (1 = no split-K).
+constexpr int SPLITK_WN = 2;         // 128 x 128 tiles
+constexpr int SPLITK_TW = 4;         // of 8 waves (64 x 32 each, two per SIMD)
+constexpr int SPLITK_TARGET = 256;   // work-groups the split grid may not exceed (one per CU)
 static int splitk_splits(int M, int N, int K) {
   if (M > 256 || N % (64 * SPLITK_WN) != 0) return 1;
   const int tiles = (N / (64 * SPLITK_WN)) * ((M + TB_M - 1) / TB_M);
   const int nkb = K / TB_K;
   int s = 1;
-  while (tiles * s < SPLITK_TARGET && s * 2 <= nkb / 2) s *= 2;
+  while (tiles * s * 2 <= SPLITK_TARGET && s * 2 <= nkb / 2) s *= 2;
   return s;
 }
 
@@ -577,8 +593,8 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
     p.partial = static_cast<float*>(ws);
     p.n_blocks = N / (64 * SPLITK_WN);
     const dim3 grid(p.n_blocks * p.m_blocks, used);
-    const int rc = M % TB_M == 0 ? launch_tiled<false, false, SPLITK_WN, true, true>(p, grid, st, f8)
-                                 : launch_tiled<false, false, SPLITK_WN, true, false>(p, grid, st, f8);
+    const int rc = M % TB_M == 0 ? launch_tiled<false, false, SPLITK_WN, true, true, SPLITK_TW>(p, grid, st, f8)
+                                 : launch_tiled<false, false, SPLITK_WN, true, false, SPLITK_TW>(p, grid, st, f8);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
