@@ -66,7 +66,7 @@ FAMILIES = {
     "moe_ep8_prefill": [f"dsv3_ep8_{p}_M{m}" for m in (64, 128, 256, 512) for p in ("gate_up", "down")],
     "kimi_tp8": ["kimi_w4a16_w13_T8_tp8"],
 }
-DENSE_KINDS = ("linear_bf16", "fp8_gemm", "quant_act", "moe_combine")
+DENSE_KINDS = ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0", "quant_act", "moe_combine")
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(
     FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
@@ -97,11 +97,14 @@ class Runner:
             self.copies += [{k: v.clone() for k, v in self.inp.items()} for _ in range(ncopy - 1)]
         self.ws = None
         self.n_hit = 0
-        if wl.kind in ("linear_bf16", "fp8_gemm"):
+        if wl.kind in ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0"):
             shape = (wl.M, wl.N)
             self.outs = [torch.empty(shape, dtype=torch.bfloat16, device="cuda") for _ in self.copies]
             if wl.kind == "fp8_gemm" and ops.fp8_workspace_bytes(wl.M, wl.N, wl.K):
                 self.ws = torch.empty(ops.fp8_workspace_bytes(wl.M, wl.N, wl.K), dtype=torch.uint8, device="cuda")
+            if wl.kind == "fp8_gemm_ue8m0":
+                self.ws = torch.empty(ops.fp8_ue8m0_workspace_bytes(wl.M, wl.N, wl.K), dtype=torch.uint8,
+                                      device="cuda")
         elif wl.kind == "quant_act":
             self.outs = [(torch.empty((wl.M, wl.K), dtype=torch.float8_e4m3fn, device="cuda"),
                           torch.empty((wl.M, wl.K // 128), dtype=torch.float32, device="cuda")) for _ in self.copies]
@@ -128,6 +131,8 @@ class Runner:
             ops.linear_bf16(c["x"], c["w"], residual=c.get("r"), out=o)
         elif wl.kind == "fp8_gemm":
             ops.fp8_gemm_blockscale(c["a"], c["sa"], c["b"], c["sb"], out=o, workspace=self.ws)
+        elif wl.kind == "fp8_gemm_ue8m0":
+            ops.fp8_gemm_ue8m0(c["a"], c["sfa"], c["b"], c["sfb"], out=o, workspace=self.ws)
         elif wl.kind == "moe_fp8":
             ops.moe_w13_fp8(c["x"], c["sx"], c["w"], c["sw"], self.rt, out=o)
         elif wl.kind == "moe_fp8_w2":
@@ -170,7 +175,7 @@ def roofline_of(wl, runner, kernel_ms: float) -> dict:
     """
     unit, bound = unit_of(wl)
     ai = runner.flops / max(runner.bytes, 1)
-    fp8 = wl.kind in ("fp8_gemm", "moe_fp8", "moe_fp8_w2")
+    fp8 = wl.kind in ("fp8_gemm", "fp8_gemm_ue8m0", "moe_fp8", "moe_fp8_w2")
     mfma_peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     tflops = runner.flops / (kernel_ms * 1e-3) / 1e12
     gbps = runner.bytes / (kernel_ms * 1e-3) / 1e9
@@ -266,6 +271,19 @@ def _sample(wl, runner):
         rb = bits16(inp["r"]) if "r" in inp else None
         return (lambda: G.linear_bf16(xb, wb, rb), lambda: TC.linear_bf16(xb, wb, rb), got_all,
                 2 * wl.M * wl.N * wl.K, runner.bytes, f"all {wl.M} rows x {wl.N} outputs", False)
+    if wl.kind == "fp8_gemm_ue8m0":
+        from oracle import ue8m0 as U
+        nrows = min(wl.M, 512)
+        rows = np.sort(rng.choice(wl.M, size=nrows, replace=False)) if nrows < wl.M else np.arange(wl.M)
+        a, b = codes(inp["a"])[rows], codes(inp["b"])
+        # the scales as the kernel sees them: the packed bytes, decoded
+        nk = wl.K // 128
+        sa = U.ue8m0_to_float(U.unpack_sf(inp["sfa"].cpu().numpy().view(np.uint32), nk))[rows]
+        sb = U.ue8m0_to_float(U.unpack_sf(inp["sfb"].cpu().numpy().view(np.uint32), nk))[::128]
+        assert np.array_equal(sa, U.ue8m0_to_float(U.float_to_ue8m0(inp["sa"].cpu().numpy()[rows])))
+        return (lambda: G.fp8_blockscale_gemm(a, sa, b, sb), lambda: TC.fp8_blockscale_gemm(a, sa, b, sb),
+                got_all[rows], 2 * nrows * wl.N * wl.K, nrows * wl.K * 1 + wl.N * wl.K + nrows * wl.N * 2,
+                f"{nrows} of {wl.M} rows x all {wl.N} outputs", False)
     if wl.kind == "fp8_gemm":
         nrows = min(wl.M, 1024)
         rows = np.sort(rng.choice(wl.M, size=nrows, replace=False)) if nrows < wl.M else np.arange(wl.M)
@@ -485,7 +503,8 @@ def driver_mode(args) -> int:
 
 
 def dtype_of(wl) -> str:
-    return {"linear_bf16": "bf16", "fp8_gemm": "e4m3 (fp32 accumulate)", "moe_fp8": "e4m3 (fp32 accumulate)",
+    return {"linear_bf16": "bf16", "fp8_gemm": "e4m3 (fp32 accumulate)",
+            "fp8_gemm_ue8m0": "e4m3, UE8M0 block scales (fp32 accumulate)", "moe_fp8": "e4m3 (fp32 accumulate)",
             "moe_w4a16": "int4 weights x bf16 (fp32 accumulate)", "moe_fp8_w2": "e4m3 (fp32 accumulate)",
             "quant_act": "bf16 -> e4m3 (fp32 scale)", "moe_combine": "bf16 (fp32 accumulate)"}[wl.kind]
 
@@ -583,7 +602,8 @@ def main(argv=None) -> int:
     if args.also is None:
         args.also = [k for k in ("dsv3_fp8_M16", "dsv3_fp8_M128", "qwen3_gateup_M16", "dsv3_moe_w13_decode",
                                  "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill", "dsv3_moe_w2_decode",
-                                 "dsv3_moe_w2_prefill", "moe_quant_act_prefill", "moe_combine_prefill")
+                                 "dsv3_moe_w2_prefill", "moe_quant_act_prefill", "moe_combine_prefill",
+                                 "dsv3_o_proj_M4096_ue8m0")
                      ] if args.workload == DEFAULT_WORKLOAD else []
     import torch
     if not torch.cuda.is_available():

@@ -19,7 +19,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libferret_hip.so")
-SOURCES = ["skinny.hip", "fp8_tiled.hip", "fp8_square.hip", "routing.hip", "moe_tail.hip", "dispatch.hip"]
+SOURCES = ["skinny.hip", "fp8_tiled.hip", "fp8_square.hip", "routing.hip", "moe_tail.hip", "ue8m0.hip",
+           "dispatch.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

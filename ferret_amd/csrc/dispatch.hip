@@ -13,6 +13,7 @@ int ferret_fp8_gemm_square(const void* a, const float* sa, const void* b, const 
                            int K, hipStream_t st);
 size_t ferret_linear_bf16_workspace(int M, int N, int K);
 size_t ferret_moe_permute_workspace(long long num_pairs, int E);
+size_t ferret_fp8_gemm_ue8m0_workspace(int M, int N, int K);
 int ferret_moe_w13_fp8_skinny(const void* x, const float* sx, const void* w, const float* sw,
                               const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
                               int max_tiles, int topk, int N, int K, void* out, hipStream_t st);
@@ -46,6 +47,8 @@ extern "C" size_t ferret_workspace_bytes(int op, int M, int N, int K, int E) {
     return ferret_linear_bf16_workspace(M, N, K);
   if (op == 1 && M > 16 && M > 0 && N > 0 && K >= 128) return ferret_fp8_gemm_workspace(M, N, K);
   if (op == 4 && M > 0 && E > 0) return ferret_moe_permute_workspace(M, E);
+  if (op == 5 && M > 0 && N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0 && K / 128 <= 128)
+    return ferret_fp8_gemm_ue8m0_workspace(M, N, K);
   return 0;
 }
 

@@ -22,6 +22,7 @@ SIGNATURES = {
     "launch_gemv": (None, [_vp, _vp, _vp, _vp, _c_int, _c_int, _vp]),
     "ferret_linear_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t, _vp]),
     "ferret_fp8_gemm_blockscale": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t, _vp]),
+    "ferret_fp8_gemm_ue8m0": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size_t, _vp]),
     "ferret_moe_route_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "ferret_moe_permute": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp,
                                     _c_size_t, _vp]),

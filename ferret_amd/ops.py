@@ -134,6 +134,86 @@ def fp8_gemm_blockscale(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: 
     return out
 
 
+_SQRT_HALF = 2.0 ** -0.5
+
+
+def ue8m0_from_float(scales: torch.Tensor) -> torch.Tensor:
+    """UE8M0 bytes (uint8) of fp32 scales: the exponent byte of the power of
+    two nearest in log2 (float_to_ue8m0,
+    examples/fp8-gemm/v009_large_m_block_scale_mma_080.cu:375-384), taken from
+    the mantissa (nearer the upper power when it is >= 2^-0.5) rather than
+    from a rounded logarithm.  s <= 0 gives 0; +inf and NaN give 255; the
+    exponent is clamped to the byte (subnormal powers 0, 2^128 and up 255).
+    Host-side preparation of inputs, any device."""
+    x = scales.to(torch.float32)
+    m, e = torch.frexp(torch.where(torch.isfinite(x) & (x > 0), x, torch.ones_like(x)))
+    k = e.to(torch.int64) - 1 + (m.to(torch.float64) >= _SQRT_HALF).to(torch.int64)  # exact: no float is 2^-0.5
+    byte = torch.where(x > 0, (k + 127).clamp(0, 255), torch.zeros_like(k))
+    byte = torch.where(torch.isnan(x) | (x == float("inf")), torch.full_like(k, 255), byte)
+    return byte.to(torch.uint8)
+
+
+def pack_ue8m0(ue: torch.Tensor) -> torch.Tensor:
+    """UE8M0 bytes [dim, nk] -> int32 words [ceil(nk/4), dim] (prepare_sf,
+    v009:386-403): byte j of word [sk, d] is ue[d, 4 sk + j], missing K-blocks 0."""
+    if ue.dtype != torch.uint8 or ue.dim() != 2:
+        raise ValueError("ue must be uint8 [dim, nk]")
+    dim, nk = ue.shape
+    nsk = (nk + 3) // 4
+    padded = torch.zeros((dim, nsk * 4), dtype=torch.uint8, device=ue.device)
+    padded[:, :nk] = ue
+    return padded.view(dim, nsk, 4).permute(1, 0, 2).contiguous().view(torch.int32).view(nsk, dim)
+
+
+def expand_block_scales(sb: torch.Tensor, N: int) -> torch.Tensor:
+    """Weight block scales [ceil(N/128), nk] -> one row per weight row [N, nk]
+    (expand_sb, v009:405-412)."""
+    if sb.dim() != 2 or sb.shape[0] != (N + 127) // 128:
+        raise ValueError("sb must be [ceil(N/128), nk]")
+    return sb.repeat_interleave(128, dim=0)[:N].contiguous()
+
+
+def fp8_ue8m0_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes ferret_fp8_gemm_ue8m0 needs (decoded scales + split-K partials)."""
+    return int(_lib.load().ferret_workspace_bytes(5, M, N, K, 0))
+
+
+def fp8_gemm_ue8m0(a: torch.Tensor, sfa: torch.Tensor, b: torch.Tensor, sfb: torch.Tensor,
+                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """c[M,N] (bf16) = a[M,K] (e4m3) . b[N,K]^T (e4m3) with UE8M0 block scales.
+
+    sfa: int32 words [ceil(nk/4), M] and sfb: int32 words [ceil(nk/4), N] in
+    the reference's packed layout (pack_ue8m0 of ue8m0_from_float, sfb over
+    expand_block_scales); nk = K/128.  A workspace of fp8_ue8m0_workspace_bytes
+    is taken from torch's caching allocator unless one is passed.
+    """
+    _dev(a, "a", (FP8, torch.uint8), 2)
+    _dev(b, "b", (FP8, torch.uint8), 2)
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError("b must be [N, K]")
+    nsk = (K // 128 + 3) // 4
+    if tuple(sfa.shape) != (nsk, M) or tuple(sfb.shape) != (nsk, N):
+        raise ValueError(f"packed scales must be sfa [{nsk}, M], sfb [{nsk}, N]; got {tuple(sfa.shape)}, "
+                         f"{tuple(sfb.shape)}")
+    _same_device(a, sfa, b, sfb, out, workspace)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _out(out, "out", (M, N), torch.bfloat16, a.device)
+    need = fp8_ue8m0_workspace_bytes(M, N, K)
+    if need == 0:
+        raise ValueError(f"unsupported shape M={M} N={N} K={K}")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+    rc = _lib.load().ferret_fp8_gemm_ue8m0(
+        _dev(a, "a", (FP8, torch.uint8), 2), _dev(sfa, "sfa", torch.int32, 2), _dev(b, "b", (FP8, torch.uint8), 2),
+        _dev(sfb, "sfb", torch.int32, 2), _dev(out, "out", torch.bfloat16, 2), M, N, K,
+        _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(), _stream())
+    _lib.check("ferret_fp8_gemm_ue8m0", rc)
+    return out
+
+
 def moe_route_topk(logits: torch.Tensor, topk: int, with_weights: bool = True):
     """ids int32 [T, topk] (logit desc, expert asc) and softmax weights [T, topk]."""
     T, E = logits.shape

@@ -27,7 +27,7 @@ FP8 = torch.float8_e4m3fn
 @dataclass(frozen=True)
 class Workload:
     key: str
-    kind: str            # "linear_bf16" | "fp8_gemm" | "moe_fp8" | "moe_w4a16" | "moe_fp8_w2"
+    kind: str            # "linear_bf16" | "fp8_gemm" | "fp8_gemm_ue8m0" | "moe_fp8" | "moe_w4a16" | "moe_fp8_w2"
                          # | "quant_act" | "moe_combine"
     M: int = 0           # dense tokens
     N: int = 0           # output rows (per expert: gate + up)
@@ -64,6 +64,16 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
              description="DeepSeek-V3 dense FP8 GEMM M=128", seeds={"a": 3, "b": 4}),
     Workload("dsv3_fp8_M4096", "fp8_gemm", M=4096, N=4096, K=7168, bound="mfma",
              description="DeepSeek-V3 dense FP8 GEMM M=4096", seeds={"a": 3, "b": 4}),
+    # UE8M0 block-scale mode on the reference's block-scale configs
+    # (examples/fp8-gemm/v009_large_m_block_scale_mma_080.cu:526-532): random
+    # e4m3 codes and scales drawn as 0.5 + (rand() % 100) / 200 (:549-552),
+    # rounded to powers of two and packed the reference's way.
+    *[Workload(f"dsv3_{proj}_M{m}_ue8m0", "fp8_gemm_ue8m0", M=m, N=n, K=k, bound="mfma",
+               description=f"DeepSeek-V3 {proj} FP8 GEMM with UE8M0 block scales: A e4m3 [{m},{k}], B e4m3 [{n},{k}]",
+               seeds={"a": 50 + i, "b": 54 + i})
+      for i, (proj, m, k, n) in enumerate([("o_proj", 2048, 2048, 7168), ("q_b_proj", 8192, 1536, 3072),
+                                           ("kv_b_proj", 8192, 512, 4096), ("o_proj", 4096, 2048, 7168),
+                                           ("o_proj", 8192, 2048, 7168)])],
     # DeepSeek-V3 attention projections at TP = 8 (per-rank shapes): decode and
     # a 512-token chunk (tasks/fp8-gemm-dense-tp8.yaml:36-74) and prefill with
     # M up to the 8K kv_len of kv_b_proj (tasks/fp8-gemm-prefill-tp8.yaml:44-117).
@@ -176,6 +186,22 @@ def make_inputs(w: Workload, device="cuda", experts: list[int] | None = None) ->
         a, sa = quant_act_1x128(randn((w.M, w.K), s["a"], device))
         b, sb = quant_weight_128x128(randn((w.N, w.K), s["b"], device))
         return {"a": a, "sa": sa, "b": b, "sb": sb}
+    if w.kind == "fp8_gemm_ue8m0":
+        from . import ops
+        nk, nbk = w.K // 128, (w.N + 127) // 128
+
+        def codes(shape, seed):
+            c = torch.randint(0, 254, shape, generator=_gen(seed, device), device=device, dtype=torch.int32)
+            return torch.where(c >= 0x7F, c + 1, c).to(torch.uint8).view(FP8)   # no NaN codes
+
+        def scales(shape, seed):
+            r = torch.randint(0, 100, shape, generator=_gen(seed, device), device=device, dtype=torch.int32)
+            return 0.5 + r.to(torch.float32) / 200.0
+        sa, sb = scales((w.M, nk), s["a"] + 1000), scales((nbk, nk), s["b"] + 1000)
+        sfa = ops.pack_ue8m0(ops.ue8m0_from_float(sa))
+        sfb = ops.pack_ue8m0(ops.ue8m0_from_float(ops.expand_block_scales(sb, w.N)))
+        return {"a": codes((w.M, w.K), s["a"]), "b": codes((w.N, w.K), s["b"]), "sfa": sfa, "sfb": sfb,
+                "sa": sa, "sb": sb}
     if w.routing == "zipf":
         logits = zipf_logits(w.T, w.E, w.zipf_s, s["logits"], device)
     elif w.routing == "uniform":
@@ -222,6 +248,9 @@ def algorithmic_bytes(w: Workload, n_experts_hit: int = 0) -> int:
     if w.kind == "fp8_gemm":
         return (w.M * w.K + w.M * (w.K // 128) * 4 + w.N * w.K + ((w.N + 127) // 128) * (w.K // 128) * 4
                 + w.M * w.N * 2)
+    if w.kind == "fp8_gemm_ue8m0":   # packed scale words: 4 bytes per 4 K-blocks, per token / weight row
+        nsk = (w.K // 128 + 3) // 4
+        return w.M * w.K + w.N * w.K + (w.M + w.N) * nsk * 4 + w.M * w.N * 2
     P = w.T * w.topk
     if w.kind == "moe_fp8":
         per_e = w.N * w.K + (w.N // 128) * (w.K // 128) * 4
@@ -241,7 +270,7 @@ def algorithmic_bytes(w: Workload, n_experts_hit: int = 0) -> int:
 
 
 def flops(w: Workload) -> int:
-    if w.kind in ("linear_bf16", "fp8_gemm"):
+    if w.kind in ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0"):
         return 2 * w.M * w.N * w.K
     if w.kind == "quant_act":
         return 2 * w.M * w.K               # one scale multiply + one |x| max per element

@@ -99,6 +99,26 @@ int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, co
                                void* stream);
 
 /*
+ * Dense FP8 GEMM with UE8M0 (power-of-two) block scales in the packed layout
+ * of examples/fp8-gemm/v009_large_m_block_scale_mma_080.cu (prepare_sf
+ * :386-403, expand_sb :405-412); replaces its run_bs / dispatch_run
+ * (:414-476, :507-515):
+ *   sfa uint32 [ceil(nk/4), M] column-major, byte j of word sfa[sk*M + m] the
+ *       scale of token m for K-block 4*sk + j (nk = K/128);
+ *   sfb uint32 [ceil(nk/4), N], per weight row (expand_sb's layout: the rows of
+ *       a 128-row block carry the same bytes; row 128*(n/128) is read).
+ * A byte e stands for 2^(e-127) and e = 0 for a zero scale (ue8m0_to_float,
+ * :478-484), so c[m,n] = sum_kb (sum_{k in kb} a[m,k] b[n,k]) * 2^(ea-127) *
+ * 2^(eb-127), the reference's oracle ref_bs (:486-505).  a e4m3 [M,K],
+ * b e4m3 [N,K], c bf16 [M,N]; requirements as ferret_fp8_gemm_blockscale.
+ * `ws` is required: at least ferret_workspace_bytes(5, M, N, K, 0) bytes (the
+ * scales decoded to fp32, then the GEMM's split-K partials); a smaller one
+ * returns FERRET_ERR_WORKSPACE.
+ */
+int ferret_fp8_gemm_ue8m0(const void* a, const uint32_t* sfa, const void* b, const uint32_t* sfb, void* c,
+                          int M, int N, int K, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Top-k routing on fp32 logits [T,E]: ids[T,topk] (int32) ordered by
  * (logit desc, expert asc), NaN ranks as -inf; weights[T,topk] (optional,
  * may be NULL) = softmax over all E at the chosen experts.  The reference has
@@ -238,7 +258,8 @@ int ferret_moe_w2_fp8_ex(const void* h, const float* sh, const void* w, const fl
 
 /* Workspace bytes an op can use (0 = none). op: 0 linear_bf16 (split-K partials),
  * 1 fp8_gemm_blockscale (split-K partials for 16 < M <= 256), 2 moe_w13_fp8,
- * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts). */
+ * 3 moe_w13_w4a16, 4 moe_permute (M = number of routed pairs P, E experts),
+ * 5 fp8_gemm_ue8m0 (decoded scales + split-K partials; required). */
 size_t ferret_workspace_bytes(int op, int M, int N, int K, int E);
 
 #ifdef __cplusplus

@@ -92,3 +92,21 @@ def test_python_ops_refuse_cpu_tensors():
     w = torch.zeros((16, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.linear_bf16(x, w, out=torch.zeros((1, 16), dtype=torch.bfloat16))
+
+
+def test_ue8m0_gemm_rejects_before_launch():
+    """ferret_fp8_gemm_ue8m0 validates pointers, shapes and its (required)
+    workspace on the host and returns before any HIP call (pointers here are
+    never dereferenced)."""
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    L = lib.load()
+    need = L.ferret_workspace_bytes(5, 256, 4096, 7168, 0)
+    assert need >= 256 * 56 * 4 + 32 * 56 * 4
+    assert L.ferret_fp8_gemm_ue8m0(None, 1, 1, 1, 1, 256, 4096, 7168, 1, need, None) == -1
+    assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4096, 7100, 1, need, None) == -2
+    assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4000, 7168, 1, need, None) == -2
+    assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4096, 7168, None, 0, None) == -3
+    assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4096, 7168, 1, need - 1, None) == -3
+    assert L.ferret_workspace_bytes(5, 256, 4096, 7100, 0) == 0
