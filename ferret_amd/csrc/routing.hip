@@ -10,7 +10,8 @@
 //   * top-k by (logit desc, expert asc), NaN ranked as -inf;
 //   * pair p = t*topk + j; pairs of one expert keep ascending pair order
 //     (computed with wave ballots, never from atomic arrival order);
-//   * tiles (expert, first sorted row, rows <= tile_m), expert-major.
+//   * tiles (expert, first sorted row, rows <= tile_m), expert-major; the
+//     entries past the last tile up to max_tiles are (0, 0, 0).
 #include "common.hpp"
 
 namespace ferret {
@@ -142,6 +143,13 @@ __device__ void permute_tables(const int* cnt, int* scan, int* tscan, int* curso
         tiles[3 * tt + 2] = min(tile_m, c - j);
       }
     }
+  }
+  // Entries past the last tile up to max_tiles are zero (expert 0, row 0, no
+  // rows), so the whole table is a function of the ids.
+  for (int t = tscan[E - 1] + tid; t < max_tiles; t += blockDim.x) {
+    tiles[3 * t] = 0;
+    tiles[3 * t + 1] = 0;
+    tiles[3 * t + 2] = 0;
   }
   __syncthreads();
 }

@@ -137,7 +137,8 @@ int ferret_moe_route_topk(const float* logits, int T, int E, int topk, int32_t* 
  * Outputs: counts[E], offsets[E+1] (exclusive cumsum), sorted_pair[P] (pairs
  * of expert 0 in ascending order, then expert 1, ...; ids outside [0,E) are
  * dropped), tiles[max_tiles*3] rows (expert, first sorted row, rows <= tile_m)
- * in expert order, ntiles[1].  max_tiles must be >= ferret_moe_max_tiles().
+ * in expert order (rows past the last tile are (0, 0, 0)), ntiles[1].
+ * max_tiles must be >= ferret_moe_max_tiles().
  * `ws` (optional): with at least ferret_workspace_bytes(4, P, 0, 0, E) bytes
  * the work is spread over one work-group per 1024 pairs (same output); with
  * NULL one work-group does it all (fine for decode-sized P).

@@ -1,0 +1,70 @@
+"""The torch.library layer (ferret_amd.torch_ops) without a GPU: every op is
+registered under torch.ops.ferret, its fake implementation gives the output
+shapes and dtypes the kernels write (meta tensors), and a CPU tensor is refused
+(no CPU path)."""
+import os
+
+import pytest
+import torch
+
+from ferret_amd import lib
+
+
+def _ops():
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    import ferret_amd.torch_ops as T
+    return T
+
+
+def test_every_op_is_registered():
+    T = _ops()
+    for name in T.OPS:
+        assert hasattr(torch.ops.ferret, name), name
+
+
+def m(*shape, dtype=torch.float32):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def test_fake_shapes_dense():
+    _ops()
+    F = torch.ops.ferret
+    bf, f8, i32 = torch.bfloat16, torch.float8_e4m3fn, torch.int32
+    y = F.linear_bf16(m(16, 4096, dtype=bf), m(6144, 4096, dtype=bf), None)
+    assert y.shape == (16, 6144) and y.dtype == bf
+    c = F.fp8_gemm_blockscale(m(300, 7168, dtype=f8), m(300, 56), m(4096, 7168, dtype=f8), m(32, 56))
+    assert c.shape == (300, 4096) and c.dtype == bf
+    c = F.fp8_gemm_ue8m0(m(64, 2048, dtype=f8), m(4, 64, dtype=i32), m(7168, 2048, dtype=f8), m(4, 7168, dtype=i32))
+    assert c.shape == (64, 7168)
+    q, s = F.quant_act_e4m3(m(32768, 2048, dtype=bf))
+    assert q.shape == (32768, 2048) and q.dtype == f8 and s.shape == (32768, 16) and s.dtype == torch.float32
+
+
+def test_fake_shapes_moe():
+    _ops()
+    F = torch.ops.ferret
+    bf, f8, i32 = torch.bfloat16, torch.float8_e4m3fn, torch.int32
+    ids, w = F.moe_route_topk(m(4096, 256), 8)
+    assert ids.shape == (4096, 8) and ids.dtype == i32 and w.shape == (4096, 8)
+    counts, offsets, sp, tiles, nt = F.moe_permute(m(4096, 8, dtype=i32), 256, 0)
+    assert counts.shape == (256,) and offsets.shape == (257,) and sp.shape == (32768,)
+    assert tiles.shape == (lib.load().ferret_moe_max_tiles(32768, 256, 128), 3) and nt.shape == (1,)
+    o = F.moe_w13_fp8(m(4096, 7168, dtype=f8), m(4096, 56), m(256, 4096, 7168, dtype=f8), m(256, 32, 56),
+                      sp, tiles, nt, 128, 8)
+    assert o.shape == (32768, 2048) and o.dtype == bf
+    o = F.moe_w13_w4a16(m(64, 7168, dtype=bf), m(384, 4096, 896, dtype=i32), m(384, 4096, 224, dtype=bf),
+                        m(512, dtype=i32), m(896, 3, dtype=i32), m(1, dtype=i32), 16, 8)
+    assert o.shape == (512, 2048)
+    o2 = F.moe_w2_fp8(m(32768, 2048, dtype=f8), m(32768, 16), m(256, 7168, 2048, dtype=f8), m(256, 56, 16),
+                      sp, tiles, nt, 128, 8)
+    assert o2.shape == (32768, 7168)
+    y = F.moe_combine(m(32768, 7168, dtype=bf), m(4096, 8))
+    assert y.shape == (4096, 7168) and y.dtype == bf
+
+
+def test_cpu_tensors_are_refused():
+    _ops()
+    with pytest.raises(ValueError, match="GPU tensor"):
+        torch.ops.ferret.linear_bf16(torch.zeros(1, 128, dtype=torch.bfloat16),
+                                     torch.zeros(16, 128, dtype=torch.bfloat16), None)
