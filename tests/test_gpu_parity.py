@@ -89,6 +89,50 @@ def test_linear_bf16_split_k_and_residual_paths(hip, M, N, K, res):
         assert nbad == 0 and e < 5e-3, f"{tag}: {e}"
 
 
+@pytest.mark.parametrize("M,N,K,res", [(16, 6144, 4096, False), (16, 4096, 12288, True), (1, 6144, 4096, True)])
+def test_linear_bf16_split_k_fixup_workspace_contract(hip, M, N, K, res):
+    """Split-K products over a caller workspace: it needs no initialisation
+    (filled with random bits here), one workspace serves consecutive calls,
+    and a HIP graph replays the call (GEMM + split reduce) with eager calls on
+    the same workspace in between -- every result bit-identical to the first."""
+    _say(f"linear_bf16 split-K fix-up M={M} N={N} K={K} res={res}")
+    g = torch.Generator(device="cuda").manual_seed(M * 5 + N + K)
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    r = torch.randn((M, N), generator=g, device="cuda").to(torch.bfloat16) if res else None
+    need = int(hip.ferret_workspace_bytes(0, M, N, K, 0))
+    assert need > 0, "shape expected to split K"
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device="cuda", generator=g)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def call(y):
+        return hip.ferret_linear_bf16(x.data_ptr(), w.data_ptr(), r.data_ptr() if res else None, y.data_ptr(),
+                                      M, N, K, ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+
+    ys = [torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    for y in ys:
+        assert call(y) == 0
+    torch.cuda.synchronize()
+    ref = G.linear_bf16(bits16(x), bits16(w), bits16(r) if res else None)
+    e, nbad = MT.linear_rel_err(bf16_out(ys[0]), ref)
+    assert nbad == 0 and e < 5e-3
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    yg = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        assert call(yg) == 0
+    for i in range(4):
+        yg.fill_(float("nan"))
+        assert call(ys[1]) == 0            # eager work on the same workspace between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ys[0]) and torch.equal(ys[1], ys[0]), f"replay {i}"
+    del st
+
+
 def test_launch_gemv_compat(hip):
     """The reference ctypes ABI (M = 1) writes the same result as ferret_linear_bf16."""
     N, K = 256, 1024
