@@ -148,6 +148,34 @@ def test_moe_combine_matches_oracle(ops, T, topk, N):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + mag * 2.0 ** -20)
 
 
+def test_tail_workloads_at_bench_size(ops):
+    """The bench's prefill tail workloads at full size: the quantizer on bf16
+    [32768, 2048] bit-exact over every row, the top-8 combine of [32768, 7168]
+    on 512 sampled tokens within the combine bound."""
+    from ferret_amd import workloads as W
+    _say("moe_quant_act_prefill at full size")
+    wl = W.WORKLOADS["moe_quant_act_prefill"]
+    x = W.make_inputs(wl, "cuda")["x"]
+    q, s = ops.quant_act_e4m3(x)
+    torch.cuda.synchronize()
+    rq, rs = Q.quant_act_1x128(bf16_out(x))
+    assert np.array_equal(codes8(q), rq)
+    assert np.array_equal(f32(s).view(np.uint32), rs.view(np.uint32))
+    del x, q, s
+    _say("moe_combine_prefill at full size")
+    wl = W.WORKLOADS["moe_combine_prefill"]
+    inp = W.make_inputs(wl, "cuda")
+    y = ops.moe_combine(inp["o"], inp["w"])
+    torch.cuda.synchronize()
+    toks = np.sort(np.random.default_rng(0).choice(wl.T, 512, replace=False))
+    rows = (toks[:, None] * wl.topk + np.arange(wl.topk)[None, :]).reshape(-1)
+    ob, wts = bits16(inp["o"])[rows], f32(inp["w"])[toks]
+    ref = G.moe_combine(ob, wts)
+    got = bf16_out(y)[toks]
+    mag = (np.abs(wts)[:, :, None] * np.abs(F.bf16_bits_to_f32(ob)).reshape(len(toks), wl.topk, wl.N)).sum(axis=1)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + mag * 2.0 ** -20)
+
+
 def test_moe_combine_one_hot_weights_select_rows_exactly(ops):
     _say("moe_combine one-hot")
     T, topk, N = 50, 8, 256
