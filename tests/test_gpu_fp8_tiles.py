@@ -105,6 +105,37 @@ def test_fp8_mma_precision_dense(ops, key):
     assert errs["e4m3"] >= MARGIN, f"{key}: the FP8 MFMA meets the {MARGIN} margin here; dispatch it"
 
 
+def test_vendor_fp8_gemm_misses_the_gate_too(ops):
+    """The vendor library's FP8 GEMM (hipBLASLt through torch._scaled_mm, unit
+    scales, so only the matrix cores' summation differs from the fp32 oracle)
+    misses the reference's 1e-2 gate on the headline operands, with the same
+    error as this library's opt-in FP8-MFMA instance; the exact-widening path
+    meets it.  Recorded evidence for dispatching the bf16 path: the limit is
+    the FP8 MFMA, not this library's use of it."""
+    from ferret_amd import workloads as W
+    wl = W.WORKLOADS["dsv3_fp8_M4096"]
+    inp = W.make_inputs(wl, "cuda")
+    rows = np.sort(np.random.default_rng(0).choice(wl.M, 128, replace=False))
+    ones_a, ones_b = torch.ones_like(inp["sa"]), torch.ones_like(inp["sb"])
+    ref = G.fp8_blockscale_gemm(codes8(inp["a"])[rows], f32(ones_a)[rows], codes8(inp["b"]), f32(ones_b))
+    one = torch.tensor(1.0, device="cuda")
+    try:
+        y = torch._scaled_mm(inp["a"], inp["b"].t(), scale_a=one, scale_b=one, out_dtype=torch.float32)
+    except (RuntimeError, NotImplementedError) as ex:
+        pytest.skip(f"torch._scaled_mm unavailable: {ex}")
+    torch.cuda.synchronize()
+    vendor, _ = MT.fp8_rel_err(y.cpu().numpy()[rows], ref)
+    errs = {}
+    for mma in ("bf16", "e4m3"):
+        c = ops.fp8_gemm_blockscale(inp["a"], ones_a, inp["b"], ones_b, mma=mma)
+        torch.cuda.synchronize()
+        errs[mma], _ = MT.fp8_rel_err(bf16_out(c)[rows], ref)
+    _say(f"FP8 GEMM precision at K=7168: hipBLASLt fp8 {vendor:.5f}, this library fp8 mfma {errs['e4m3']:.5f}, "
+         f"exact widening {errs['bf16']:.5f}")
+    assert errs["bf16"] < MARGIN
+    assert vendor >= MARGIN and errs["e4m3"] >= MARGIN
+
+
 @pytest.mark.parametrize("key", ["dsv3_moe_w13_prefill", "dsv3_moe_w2_prefill"])
 def test_fp8_mma_precision_moe_prefill(ops, key):
     from ferret_amd import workloads as W
