@@ -117,6 +117,11 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   constexpr int ROWB = StreamFmt<F>::kRowB;
   constexpr int NI = StreamFmt<F>::kInstr;
   constexpr int L = C::kLoads;
+  // Paired refills for the 4-wave bf16 configuration (>= 4 row units per CU:
+  // GateUp 34.9 -> 34.4 us, LMHead 192.5 -> 189.0 us; the 8-wave split-K
+  // products and the FP8 kernels measured no gain).  They need units of an even
+  // number of K-steps (step parity = item parity) and >= 3 ring stages.
+  constexpr bool PAIR = F == kBF16 && NW == 4 && KS % 2 == 0 && D >= 3;
   static_assert(EPI != kSilu || RB == 2, "SiLU units pair one gate and one up block");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
@@ -363,15 +368,26 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       const int it = (u - u_begin) * KS + s;
       StepFrag<F, RB> nxt;
       if constexpr (s + 1 < KS) {
-        // Wait for step s+1's stage (items issued after it may stay in flight).
-        wait_items<L, SI, KS, s + 1, (D >= 2 ? D - 2 : 0)>(min(D - 2, n_items - 2 - it));
+        // Wait for step s+1's stage (items issued after it may stay in flight:
+        // D - 2, one fewer after an even step when refills go out in pairs).
+        constexpr int NY = (D >= 2 ? D - 2 : 0) - ((PAIR && (s & 1) != 0) ? 1 : 0);
+        wait_items<L, SI, KS, s + 1, NY>(min(NY, n_items - 2 - it));
         __builtin_amdgcn_sched_barrier(0);
         load_frag(nxt, (it + 1) % D, s + 1);
       }
       compute(cur, sc);
       __builtin_amdgcn_sched_barrier(0);
-      // Refill the slot of step s (its fragments were consumed above).
-      if (it + D < n_items) issue(it % D);
+      // Refill the slot of step s (its fragments were consumed above).  Paired:
+      // after each odd step refill the slots of both steps, so the wave asks for
+      // two consecutive K-steps (512 B) of each of its rows at once.
+      if constexpr (PAIR) {
+        if constexpr ((s & 1) != 0) {
+          if (it - 1 + D < n_items) issue((it - 1) % D);
+          if (it + D < n_items) issue(it % D);
+        }
+      } else {
+        if (it + D < n_items) issue(it % D);
+      }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (s + 1 < KS) cur = nxt;
     });
