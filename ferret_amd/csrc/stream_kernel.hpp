@@ -54,6 +54,9 @@ struct StreamCfg {
   // FP8: + 256 B per stage for the 128 x 128 weight-block scale of each row block.
   static constexpr int kStage = kWBytes + (F == kFP8 ? 256 : 0);
   static constexpr int kLoads = RB * StreamFmt<F>::kInstr + (F == kFP8 ? 1 : 0);  // DMA ops per stage
+  // Activation loads of one K-step (vector loads: FP8 two 16-B loads and the
+  // scale, bf16 / INT4 four 16-B loads).
+  static constexpr int kXLoads = F == kFP8 ? 3 : 4;
   static constexpr int kRing = D * kStage;                            // per wave
   // INT4: the group scales of a unit (RB * 16 rows x this wave's KS K-steps,
   // 8 B per row and K-step) are copied once per unit as whole 16-B chunks:
@@ -71,7 +74,10 @@ struct StreamCfg {
   static constexpr int kLds = NW * (kRing + kScl) + 2 * kRed + kTiles;
   static_assert(F != kINT4 || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(D >= 1 && D * kLoads + kSclLoads < 64, "vmcnt range");
+  static_assert(D >= 1 && D * (kLoads + kXLoads) + kSclLoads < 64, "vmcnt range");
+  // First token tile's activations interleaved with its weight items: when the
+  // ring prologue and the first unit's refills reach at most one unit ahead.
+  static constexpr bool kInterleave = D <= KS;
 };
 
 // Chunk slot of global 16-byte chunk c of LDS row `row` (per row width).
@@ -97,6 +103,16 @@ __device__ __forceinline__ void wait_items(int n) {
     }
     wait_items<L, SI, KS, S, N - 1>(n);
   }
+}
+
+// Vector-memory ops issued after item S of the first unit of the first token
+// tile, up to item S + N: item i < KS is preceded by the LX activation loads
+// of K-step i, and the next unit's first item carries SI.
+template <int L, int LX, int SI, int KS, int S, int N>
+constexpr int first_unit_ops() {
+  int ops = 0;
+  for (int i = S + 1; i <= S + N; ++i) ops += L + (i < KS ? LX : 0) + (i % KS == 0 ? SI : 0);
+  return ops;
 }
 
 // s_waitcnt lgkmcnt(0) only (LDS writes done before a barrier).
@@ -254,7 +270,8 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   int my_pair = 0;  // grouped: routed pair of token column r (from sorted_pair)
   int nrows = 0, row0 = 0;
   int cur_split = -1;
-  auto load_tile = [&](int u) {
+  int tok = 0;  // activation row of this lane's token column
+  auto set_tile = [&](int u) {
     const int split = u / units_per_split;
     const int tile = (u % units_per_split) / a.units_n;
     cur_tile = tile;
@@ -267,48 +284,56 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       nrows = min(16, a.M - row0);
     }
     const int tcol = min(r, nrows - 1);  // columns >= nrows compute garbage, never stored
-    int tok = row0 + tcol;
+    tok = row0 + tcol;
     if (grouped) {
       my_pair = a.sorted_pair[row0 + tcol];
       tok = my_pair / a.topk;
     }
+  };
+  // Activations of this wave's K-step k of the current tile and split:
+  // C::kXLoads vector loads.
+  auto load_x = [&](int k) {
+    const int ks = (cur_split * NW + wave) * KS + k;
+    if constexpr (F == kFP8) {
+      const uint8_t* xp = a.x + (size_t)tok * K + (size_t)ks * 128 + 32 * g;
+      xv[k][0] = ld_u32x4(xp);
+      xv[k][1] = ld_u32x4(xp + 16);
+      sx[k] = a.x_scale[(size_t)tok * nkb + ks];
+    } else {
+      const uint8_t* xp = a.x + ((size_t)tok * K + (size_t)ks * 128 + 32 * g) * 2;
 #pragma unroll
-    for (int k = 0; k < KS; ++k) {
-      const int ks = (split * NW + wave) * KS + k;
-      if constexpr (F == kFP8) {
-        const uint8_t* xp = a.x + (size_t)tok * K + (size_t)ks * 128 + 32 * g;
-        xv[k][0] = ld_u32x4(xp);
-        xv[k][1] = ld_u32x4(xp + 16);
-        sx[k] = a.x_scale[(size_t)tok * nkb + ks];
-      } else {
-        const uint8_t* xp = a.x + ((size_t)tok * K + (size_t)ks * 128 + 32 * g) * 2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
-      }
+      for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
     }
   };
-  // The first tile's activations go out before the ring prologue: issued first,
-  // they complete first, and the compiler's counted wait before their first use
-  // leaves the weight stream in flight.
-  load_tile(u_begin);
-
-  set_issue_unit(iu);
+  // Pins the activations of K-step k after the wait that covers them: code that
+  // uses them (the FP8 widening) cannot be hoisted above that wait, where the
+  // compiler would wait for every load still in flight.
+  auto fence_x = [&](int k) {
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < n_items) issue(d);
-
+    for (int j = 0; j < XV; ++j) asm volatile("" : "+v"(xv[k][j]));
+    if constexpr (F == kFP8) asm volatile("" : "+v"(sx[k]));
+  };
   f32x4 acc[RB];
   int buf = 0;
 
-  for (int u = u_begin; u < u_end; ++u) {
+  // One unit.  FIRST: the work-group's first unit with more to follow, its
+  // activations interleaved with its weight items (below); its refills then
+  // always reach the next unit (D <= KS), so every issue and wait in it is
+  // unconditional and the compiler counts the vector-memory ops ahead of each
+  // activation use exactly instead of waiting for all of them.  Otherwise a
+  // unit of another token tile (or split) loads its activations all at once.
+  auto run_unit = [&](auto firstc, int u) {
+    constexpr bool first = decltype(firstc)::value;
     const int split = u / units_per_split;
     const int tile = (u % units_per_split) / a.units_n;
     const int nu = u % a.units_n;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (tile != cur_tile || split != cur_split) {
-      load_tile(u);
-      wait_vmcnt<0>();  // a later token tile: drains the ring as well
+    if (!first && (tile != cur_tile || split != cur_split)) {
+      set_tile(u);
+#pragma unroll
+      for (int k = 0; k < KS; ++k) load_x(k);
+      wait_vmcnt<0>();  // drains the ring as well
     }
 
     const uint8_t* sb_unit = sclbuf + (u & 1) * C::kSclBuf;
@@ -359,7 +384,12 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     StepFrag<F, RB> cur;
     {
       const int it0 = (u - u_begin) * KS;
-      wait_items<L, SI, KS, 0, D - 1>(min(D - 1, n_items - 1 - it0));
+      if constexpr (first) {
+        wait_vmcnt<first_unit_ops<L, C::kXLoads, SI, KS, 0, D - 1>()>();
+        fence_x(0);
+      } else {
+        wait_items<L, SI, KS, 0, D - 1>(min(D - 1, n_items - 1 - it0));
+      }
       __builtin_amdgcn_sched_barrier(0);
       load_frag(cur, it0 % D, 0);
     }
@@ -371,7 +401,12 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
         // Wait for step s+1's stage (items issued after it may stay in flight:
         // D - 2, one fewer after an even step when refills go out in pairs).
         constexpr int NY = (D >= 2 ? D - 2 : 0) - ((PAIR && (s & 1) != 0) ? 1 : 0);
-        wait_items<L, SI, KS, s + 1, NY>(min(NY, n_items - 2 - it));
+        if constexpr (first) {
+          wait_vmcnt<first_unit_ops<L, C::kXLoads, SI, KS, s + 1, NY>()>();
+          fence_x(s + 1);
+        } else {
+          wait_items<L, SI, KS, s + 1, NY>(min(NY, n_items - 2 - it));
+        }
         __builtin_amdgcn_sched_barrier(0);
         load_frag(nxt, (it + 1) % D, s + 1);
       }
@@ -380,13 +415,40 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       // Refill the slot of step s (its fragments were consumed above).  Paired:
       // after each odd step refill the slots of both steps, so the wave asks for
       // two consecutive K-steps (512 B) of each of its rows at once.
+      // In the first unit, the activations of a refilled item's K-step (when it
+      // lies in this unit) go right before it.
       if constexpr (PAIR) {
         if constexpr ((s & 1) != 0) {
-          if (it - 1 + D < n_items) issue((it - 1) % D);
-          if (it + D < n_items) issue(it % D);
+          if constexpr (first && s - 1 + D < KS) {
+            load_x(s - 1 + D);
+            __builtin_amdgcn_sched_barrier(0);
+            issue((s - 1) % D);
+          } else if constexpr (first) {
+            issue((s - 1) % D);
+          } else if (it - 1 + D < n_items) {
+            issue((it - 1) % D);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (first && s + D < KS) {
+            load_x(s + D);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(s % D);
+          } else if constexpr (first) {
+            issue(s % D);
+          } else if (it + D < n_items) {
+            issue(it % D);
+          }
         }
       } else {
-        if (it + D < n_items) issue(it % D);
+        if constexpr (first && s + D < KS) {
+          load_x(s + D);
+          __builtin_amdgcn_sched_barrier(0);
+          issue(s % D);
+        } else if constexpr (first) {
+          issue(s % D);
+        } else if (it + D < n_items) {
+          issue(it % D);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (s + 1 < KS) cur = nxt;
@@ -436,7 +498,38 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       }
     }
     buf ^= 1;
+  };
+  // First token tile.  With at least two units, the activations of each K-step
+  // go out right before its weight item (the ring prologue and the first
+  // unit's refills): vector memory retires in issue order, so activations
+  // loaded ahead of the whole ring hold back every weight stage -- the
+  // work-group's first MFMA came ~5.7 us after its start at GateUp M = 16
+  // (2.6 us at FP8 M = 16).  A single unit, or a ring deeper than one unit,
+  // loads all of the tile's activations first.
+  set_tile(u_begin);
+  set_issue_unit(iu);
+  int u_next = u_begin;
+  if constexpr (C::kInterleave) {
+    if (u_end - u_begin > 1) {
+      static_for<0, D>([&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        load_x(d);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(d);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      run_unit(IntC<1>{}, u_begin);
+      u_next = u_begin + 1;
+    }
   }
+  if (u_next == u_begin) {
+#pragma unroll
+    for (int k = 0; k < KS; ++k) load_x(k);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < n_items) issue(d);
+  }
+  for (int u = u_next; u < u_end; ++u) run_unit(IntC<0>{}, u);
 }
 
 template <int F, int EPI, int RB, int NW, int KS, int D>
