@@ -108,11 +108,54 @@ __device__ __forceinline__ void wait_items(int n) {
 // Vector-memory ops issued after item S of the first unit of the first token
 // tile, up to item S + N: item i < KS is preceded by the LX activation loads
 // of K-step i, and the next unit's first item carries SI.
-template <int L, int LX, int SI, int KS, int S, int N>
-constexpr int first_unit_ops() {
+// Items issued after step s+1's item that may stay in flight while step s
+// waits for it: D - 2, one fewer at an odd step when refills go in pairs (the
+// even step before it refilled nothing).
+constexpr int ring_younger(int D, bool PAIR, int s) {
+  return (D >= 2 ? D - 2 : 0) - ((PAIR && (s & 1) != 0) ? 1 : 0);
+}
+
+constexpr int first_unit_ops(int L, int LX, int SI, int KS, int S, int N) {
   int ops = 0;
   for (int i = S + 1; i <= S + N; ++i) ops += L + (i < KS ? LX : 0) + (i % KS == 0 ? SI : 0);
   return ops;
+}
+template <int L, int LX, int SI, int KS, int S, int N>
+constexpr int first_unit_ops() {
+  return first_unit_ops(L, LX, SI, KS, S, N);
+}
+
+// Replays the first unit's issue order -- the ring prologue, then after each
+// K-step its refill (two after every odd step when PAIR), each item of this
+// unit preceded by its K-step's LX activation loads and item 0 of each unit
+// followed by its SI scale ops -- and checks that every counted wait in it
+// (first_unit_ops) leaves no op of the item it waits for, or of its
+// activations, among the ops still allowed in flight.
+template <int L, int LX, int SI, int KS, int D, bool PAIR>
+constexpr bool first_unit_waits_ok() {
+  int issued = 0;
+  int end_of[2 * 16] = {};  // one past each item's last op; items < KS + D <= 2 KS
+  auto item = [&](int i) {
+    issued += (i < KS ? LX : 0) + L + (i % KS == 0 ? SI : 0);
+    end_of[i] = issued;
+  };
+  for (int d = 0; d < D; ++d) item(d);
+  if (end_of[0] > issued - first_unit_ops(L, LX, SI, KS, 0, D - 1)) return false;
+  for (int s = 0; s < KS; ++s) {
+    if (s + 1 < KS) {
+      const int NY = ring_younger(D, PAIR, s);
+      if (end_of[s + 1] > issued - first_unit_ops(L, LX, SI, KS, s + 1, NY)) return false;
+    }
+    if (PAIR) {
+      if ((s & 1) != 0) {
+        item(s - 1 + D);
+        item(s + D);
+      }
+    } else {
+      item(s + D);
+    }
+  }
+  return true;
 }
 
 // s_waitcnt lgkmcnt(0) only (LDS writes done before a barrier).
@@ -138,6 +181,8 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   // products and the FP8 kernels measured no gain).  They need units of an even
   // number of K-steps (step parity = item parity) and >= 3 ring stages.
   constexpr bool PAIR = F == kBF16 && NW == 4 && KS % 2 == 0 && D >= 3;
+  static_assert(!C::kInterleave || first_unit_waits_ok<C::kLoads, C::kXLoads, C::kSclLoads, KS, D, PAIR>(),
+                "first unit: a counted wait leaves its item in flight");
   static_assert(EPI != kSilu || RB == 2, "SiLU units pair one gate and one up block");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
@@ -400,7 +445,7 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       if constexpr (s + 1 < KS) {
         // Wait for step s+1's stage (items issued after it may stay in flight:
         // D - 2, one fewer after an even step when refills go out in pairs).
-        constexpr int NY = (D >= 2 ? D - 2 : 0) - ((PAIR && (s & 1) != 0) ? 1 : 0);
+        constexpr int NY = ring_younger(D, PAIR, s);
         if constexpr (first) {
           wait_vmcnt<first_unit_ops<L, C::kXLoads, SI, KS, s + 1, NY>()>();
           fence_x(s + 1);
