@@ -74,7 +74,10 @@ struct StreamCfg {
   static constexpr int kLds = NW * (kRing + kScl) + 2 * kRed + kTiles;
   static_assert(F != kINT4 || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(D >= 1 && D * (kLoads + kXLoads) + kSclLoads < 64, "vmcnt range");
+  // Step s reads the fragments of step s + 1 before refilling, so item s + 1
+  // must already be in flight: at least two stages per wave.
+  static_assert(D >= 2, "ring depth");
+  static_assert(D * (kLoads + kXLoads) + kSclLoads < 64, "vmcnt range");
   // First token tile's activations interleaved with its weight items: when the
   // ring prologue and the first unit's refills reach at most one unit ahead.
   static constexpr bool kInterleave = D <= KS;
