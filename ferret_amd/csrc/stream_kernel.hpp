@@ -108,9 +108,6 @@ __device__ __forceinline__ void wait_items(int n) {
   }
 }
 
-// Vector-memory ops issued after item S of the first unit of the first token
-// tile, up to item S + N: item i < KS is preceded by the LX activation loads
-// of K-step i, and the next unit's first item carries SI.
 // Items issued after step s+1's item that may stay in flight while step s
 // waits for it: D - 2, one fewer at an odd step when refills go in pairs (the
 // even step before it refilled nothing).
@@ -118,6 +115,9 @@ constexpr int ring_younger(int D, bool PAIR, int s) {
   return (D >= 2 ? D - 2 : 0) - ((PAIR && (s & 1) != 0) ? 1 : 0);
 }
 
+// Vector-memory ops issued after item S of the first unit of the first token
+// tile, up to item S + N: item i < KS is preceded by the LX activation loads
+// of K-step i, and the next unit's first item carries SI.
 constexpr int first_unit_ops(int L, int LX, int SI, int KS, int S, int N) {
   int ops = 0;
   for (int i = S + 1; i <= S + N; ++i) ops += L + (i < KS ? LX : 0) + (i % KS == 0 ? SI : 0);
@@ -353,14 +353,6 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       for (int j = 0; j < 4; ++j) xv[k][j] = ld_u32x4(xp + 16 * j);
     }
   };
-  // Pins the activations of K-step k after the wait that covers them: code that
-  // uses them (the FP8 widening) cannot be hoisted above that wait, where the
-  // compiler would wait for every load still in flight.
-  auto fence_x = [&](int k) {
-#pragma unroll
-    for (int j = 0; j < XV; ++j) asm volatile("" : "+v"(xv[k][j]));
-    if constexpr (F == kFP8) asm volatile("" : "+v"(sx[k]));
-  };
   f32x4 acc[RB];
   int buf = 0;
 
@@ -434,7 +426,6 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       const int it0 = (u - u_begin) * KS;
       if constexpr (first) {
         wait_vmcnt<first_unit_ops<L, C::kXLoads, SI, KS, 0, D - 1>()>();
-        fence_x(0);
       } else {
         wait_items<L, SI, KS, 0, D - 1>(min(D - 1, n_items - 1 - it0));
       }
@@ -451,7 +442,6 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
         constexpr int NY = ring_younger(D, PAIR, s);
         if constexpr (first) {
           wait_vmcnt<first_unit_ops<L, C::kXLoads, SI, KS, s + 1, NY>()>();
-          fence_x(s + 1);
         } else {
           wait_items<L, SI, KS, s + 1, NY>(min(NY, n_items - 2 - it));
         }
