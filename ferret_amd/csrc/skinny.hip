@@ -93,12 +93,26 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
   const int nkb = a.K >> 7;
   static const int cand[] = {4, 7, 8, 2, 1};
   const int ks = choose_ks(nkb, cand, 5);
-  if (ks == 0) return FERRET_ERR_SHAPE;
-  const int nwaves = nkb / ks;
   const int grid = ntile_slots * a.units_n;
   if (grid <= 0) return FERRET_OK;
   // Prefetch depth kept so a wave stays within 128 VGPRs (16 waves / CU).
   constexpr int DB = (F == kBF16) ? 2 : ((F == kFP8 && RB == 1) ? 4 : (F == kFP8 ? 3 : 2));
+  if (ks == 0) {
+    // No K-step count divides K/128 into <= 16 waves (K/128 = 19, 23, 38, ...):
+    // the smallest of 2, 4, 7, 8 that fits 16 waves, the last wave ragged.
+    for (const int kr : {2, 4, 7, 8}) {
+      const int nw = (nkb + kr - 1) / kr;
+      if (nw > 16) continue;
+      switch (kr) {
+        case 2: return launch_one<F, EPI, RB, 2, 1, true>(a, grid, nw, st);
+        case 4: return launch_one<F, EPI, RB, 4, (DB < 3 ? DB : 3), true>(a, grid, nw, st);
+        case 7: return launch_one<F, EPI, RB, 7, DB, true>(a, grid, nw, st);
+        case 8: return launch_one<F, EPI, RB, 8, DB, true>(a, grid, nw, st);
+      }
+    }
+    return FERRET_ERR_SHAPE;  // K/128 > 128: rejected by every entry point first
+  }
+  const int nwaves = nkb / ks;
   switch (ks) {
     case 1: return launch_one<F, EPI, RB, 1, 0>(a, grid, nwaves, st);
     case 2: return launch_one<F, EPI, RB, 2, 1>(a, grid, nwaves, st);

@@ -87,7 +87,9 @@ __device__ __forceinline__ u32x4 dequant_int4x8(uint32_t w, const Int4Scale& k) 
   return d;
 }
 
-template <int F, int EPI, int RB, int KS, int D>
+// RAG: K/128 is not a multiple of KS; the last wave takes the remaining
+// nkb - wave * KS (< KS) K-steps, behind wave-uniform guards.
+template <int F, int EPI, int RB, int KS, int D, bool RAG = false>
 __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
   constexpr int WV = FmtTraits<F>::kWVec;
   constexpr int XV = FmtTraits<F>::kXVec;
@@ -138,6 +140,7 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
   const uint8_t* xrow = a.x + (size_t)tok * (F == kFP8 ? (size_t)K : (size_t)K * 2);
 
   const int ks0 = wave * KS;
+  const int kcnt = RAG ? min(KS, nkb - ks0) : KS;  // K-steps of this wave (>= 1)
 
   u32x4 wbuf[D + 1][RB][WV];
   u32x4 xbuf[D + 1][XV];
@@ -183,15 +186,17 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
   for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-  for (int s = 0; s < D; ++s) load(s, s);
+  for (int s = 0; s < D; ++s)
+    if (!RAG || s < kcnt) load(s, s);
   // Keep the prefetches where they are written: without these barriers the
   // scheduler sinks loads next to their first use and leaves only a few in flight.
   __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if (s + D < KS) load((s + D) % (D + 1), s + D);
+    if (s + D < KS && (!RAG || s + D < kcnt)) load((s + D) % (D + 1), s + D);
     __builtin_amdgcn_sched_barrier(0);
+    if (RAG && s >= kcnt) continue;
     const int slot = s % (D + 1);
     if constexpr (F == kBF16) {
 #pragma unroll
@@ -253,10 +258,10 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
 
 // ------------------------------------------------------------------ dispatch
 
-template <int F, int EPI, int RB, int KS, int D>
+template <int F, int EPI, int RB, int KS, int D, bool RAG = false>
 static int launch_one(const SkinnyArgs& a, int grid, int nwaves, hipStream_t st) {
   const size_t lds = (size_t)nwaves * RB * kRedBlock * sizeof(float);
-  hipLaunchKernelGGL((skinny_gemm_kernel<F, EPI, RB, KS, D>), dim3(grid), dim3(nwaves * 64), lds, st, a);
+  hipLaunchKernelGGL((skinny_gemm_kernel<F, EPI, RB, KS, D, RAG>), dim3(grid), dim3(nwaves * 64), lds, st, a);
   return (int)hipGetLastError();
 }
 
