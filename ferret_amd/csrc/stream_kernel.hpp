@@ -4,7 +4,7 @@
 //
 // Work decomposition.  A unit is (token tile, RB blocks of 16 weight rows); a
 // work-group of NW waves owns a contiguous range of units (a persistent grid
-// of ~2 work-groups per CU), and within a unit wave w takes the K-steps
+// of one work-group per CU), and within a unit wave w takes the K-steps
 // [w*KS, (w+1)*KS) (one K-step = 128 K = one fp32 scale block), so the unit's
 // partial sums meet once, in LDS, at the end of the unit.
 //
@@ -541,9 +541,9 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   // go out right before its weight item (the ring prologue and the first
   // unit's refills): vector memory retires in issue order, so activations
   // loaded ahead of the whole ring hold back every weight stage -- the
-  // work-group's first MFMA came ~5.7 us after its start at GateUp M = 16
-  // (2.6 us at FP8 M = 16).  A single unit, or a ring deeper than one unit,
-  // loads all of the tile's activations first.
+  // work-group's first MFMA came ~5.7 us after its start at GateUp M = 16.
+  // A single unit (FP8 M = 16: interleaving it measured no gain), or a ring
+  // deeper than one unit, loads all of the tile's activations first.
   set_tile(u_begin);
   set_issue_unit(iu);
   int u_next = u_begin;
