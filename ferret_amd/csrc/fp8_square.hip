@@ -94,6 +94,11 @@ struct Args {
   const uint8_t* b;   // e4m3 weights [N, K]
   const float* sb;    // [N/128, K/128]
   uint16_t* out;      // bf16 [M, N]
+  // UE8M0 mode: packed power-of-two scale bytes instead of sa / sb (word
+  // [sk, m]: token m, K-blocks 4 sk .. +3; sfb per weight row, row 128 nb
+  // standing for weight block nb)
+  const uint32_t* sfa;
+  const uint32_t* sfb;
   int M, N, K;
   int n_blocks;       // N / 256
   int m_blocks;       // ceil(M / 256)
@@ -101,6 +106,11 @@ struct Args {
 
 }  // namespace sq
 
+// U8: UE8M0 block scales.  A power-of-two scale widens exactly with the value
+// (v_cvt_scalef32_pk_bf16_fp8 multiplies by 2^(e - 127) of its scale
+// operand's exponent e, the byte itself), so both operands enter LDS already
+// scaled and the MFMAs sum absolute products: no running scale, no rescale.
+template <bool U8>
 __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
   using namespace sq;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -154,18 +164,43 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
   const int wkey = swz_key(lrow);  // the same for rows lrow + 16 i
   const int wch0 = ((2 * q) ^ wkey) << 4, wch1 = ((2 * q + 1) ^ wkey) << 4;
 
+  // UE8M0 mode: the scale word of each loaded row (4 K-blocks per byte
+  // word), fetched with the row's stage bytes; a weight row reads the word of
+  // its 128-row block.  Words past the arrays read as 0.
+  const int nsk = (nkb + 3) >> 2;
+  const __amdgpu_buffer_rsrc_t sf_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(U8 ? (loads_tokens ? p.sfa : p.sfb) : nullptr), (short)0,
+      U8 ? nsk * (loads_tokens ? p.M : p.N) * 4 : 0, 0x00020000);
+  const int sf_ld = loads_tokens ? p.M : p.N;  // words per sk row
+  const int sf_row0 = loads_tokens ? tok0 + lrow : wrow0 + (lrow & ~127);  // + 16 i (tokens)
+
   // Two stages in flight in registers (stg[st & 1]): the L2 / MALL latency
   // under load is longer than one stage's compute.
   u32x4 stg[2][4];
+  uint32_t sfw[2][4];
   auto load_part = [&](int st, int i) {
     stg[st & 1][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
         rsrc, (int)(loff + (unsigned)(16 * i * K)), st * kKS, 0));
+    if constexpr (U8) {
+      const int row = sf_row0 + (loads_tokens ? 16 * i : 0);
+      sfw[st & 1][i] = __builtin_amdgcn_raw_buffer_load_b32(sf_rsrc, row * 4, (st >> 3) * sf_ld * 4, 0);
+    }
   };
   auto write_part = [&](int st, int i) {
     uint8_t* row = lds + (st & 1) * kSlot + lds_row0 + 16 * i * kRowB;
     const u32x4& v = stg[st & 1][i];
-    *reinterpret_cast<bf16x8*>(row + wch0) = e4m3x8_to_bf16x8(v[0], v[1]);
-    *reinterpret_cast<bf16x8*>(row + wch1) = e4m3x8_to_bf16x8(v[2], v[3]);
+    if constexpr (U8) {
+      // byte of K-block st / 2; a zero byte is a zero scale (the instruction
+      // would take it as 2^-127), so its values are cleared instead
+      const uint32_t e = (sfw[st & 1][i] >> (8 * ((st >> 1) & 3))) & 0xFFu;
+      const float sc = __uint_as_float(e << 23);
+      const uint32_t m = e != 0 ? 0xFFFFFFFFu : 0u;
+      *reinterpret_cast<bf16x8*>(row + wch0) = e4m3x8_to_bf16x8_scaled(v[0] & m, v[1] & m, sc);
+      *reinterpret_cast<bf16x8*>(row + wch1) = e4m3x8_to_bf16x8_scaled(v[2] & m, v[3] & m, sc);
+    } else {
+      *reinterpret_cast<bf16x8*>(row + wch0) = e4m3x8_to_bf16x8(v[0], v[1]);
+      *reinterpret_cast<bf16x8*>(row + wch1) = e4m3x8_to_bf16x8(v[2], v[3]);
+    }
   };
 
   // ---- scales.  Token scales of the lane's 2 token columns
@@ -179,11 +214,15 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
   auto load_sa = [&](int mi, int kb) {
     return __builtin_amdgcn_raw_buffer_load_b32(sa_rsrc, sa_off, (32 * mi * nkb + kb) * 4, 0);
   };
-  const float* sbc = p.sb + (size_t)((wrow0 + wbase) >> 7) * nkb;
-  const float sb_lo = lane < nkb ? sbc[lane] : 0.f, sb_hi = 64 + lane < nkb ? sbc[64 + lane] : 0.f;
-  float sa_nx[kMI];
+  float sb_lo = 0.f, sb_hi = 0.f;
+  float sa_nx[kMI] = {};
+  if constexpr (!U8) {
+    const float* sbc = p.sb + (size_t)((wrow0 + wbase) >> 7) * nkb;
+    sb_lo = lane < nkb ? sbc[lane] : 0.f;
+    sb_hi = 64 + lane < nkb ? sbc[64 + lane] : 0.f;
 #pragma unroll
-  for (int mi = 0; mi < kMI; ++mi) sa_nx[mi] = __builtin_bit_cast(float, load_sa(mi, 0));
+    for (int mi = 0; mi < kMI; ++mi) sa_nx[mi] = __builtin_bit_cast(float, load_sa(mi, 0));
+  }
 
   // ---- running-scale accumulator: acc is in units of `unit` = sa * sb of the
   // current block (per token column); entering block kb multiplies it by
@@ -260,7 +299,7 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
     constexpr bool LOAD = !LAST_BLOCK;                  // stage st + 3 may exist
     const int st = 2 * kb + O;
     if constexpr (O == 0) zm_cur = zm_nx;
-    if constexpr (O == 1 && !LAST_BLOCK) {
+    if constexpr (O == 1 && !LAST_BLOCK && !U8) {
       enter_block(kb + 1);
       if (kb + 2 < nkb) {
 #pragma unroll
@@ -270,7 +309,7 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
     static_for<0, 32>([&](auto sc) {
       constexpr int slot = decltype(sc)::value;
       constexpr int u = slot / 8, t = slot % 8, ni = t / 2, mi = t % 2;
-      if constexpr (t == 0) mask_t(u);
+      if constexpr (t == 0 && !U8) mask_t(u);
       // rescale halves due in this slot (boundary slots 0-12: O = 1 slots
       // 26-31, then O = 0 slots 0-6)
       static_for<0, 8>([&](auto tc) {
@@ -279,7 +318,7 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
           constexpr int hf = decltype(hc)::value;
           constexpr int bs = kRescaleSlot[tt][hf];
           constexpr bool here = O == 1 ? (bs < 6 && slot == 26 + bs) : (bs >= 6 && slot == bs - 6);
-          if constexpr (here && !(O == 1 && LAST_BLOCK)) rescale_half(tt, hf);
+          if constexpr (here && !(O == 1 && LAST_BLOCK) && !U8) rescale_half(tt, hf);
         });
       });
       acc[ni][mi] = mfma32(wf[ni], tf[u & 1][mi], acc[ni][mi]);
@@ -309,11 +348,13 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
 
   // ---- prologue: block 0's unit, stage 0 in LDS, stage 1 in flight, the
   // first fragments.
-  enter_block(0);
-  zm_cur = zm_nx;
-  if (nkb > 1) {
+  if constexpr (!U8) {
+    enter_block(0);
+    zm_cur = zm_nx;
+    if (nkb > 1) {
 #pragma unroll
-    for (int mi = 0; mi < kMI; ++mi) sa_nx[mi] = __builtin_bit_cast(float, load_sa(mi, 1));
+      for (int mi = 0; mi < kMI; ++mi) sa_nx[mi] = __builtin_bit_cast(float, load_sa(mi, 1));
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) load_part(0, i);
@@ -350,8 +391,9 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
       for (int g4 = 0; g4 < 4; ++g4) {
         const f32x16& a = acc[ni][mi];
         u32x2 v;
-        v[0] = pack_bf16x2(a[4 * g4] * unit[mi], a[4 * g4 + 1] * unit[mi]);
-        v[1] = pack_bf16x2(a[4 * g4 + 2] * unit[mi], a[4 * g4 + 3] * unit[mi]);
+        const float un = U8 ? 1.0f : unit[mi];  // U8: the sums are absolute already
+        v[0] = pack_bf16x2(a[4 * g4] * un, a[4 * g4 + 1] * un);
+        v[1] = pack_bf16x2(a[4 * g4 + 2] * un, a[4 * g4 + 3] * un);
         *reinterpret_cast<u32x2*>(stgb + (32 * mi + c32) * kPitch + (32 * ni + 8 * g4 + 4 * h) * 2) = v;
       }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own rows are written
@@ -395,7 +437,27 @@ int ferret_fp8_gemm_square(const void* a, const float* sa, const void* b, const 
   p.K = K;
   p.n_blocks = N / sq::kBW;
   p.m_blocks = (M + sq::kBT - 1) / sq::kBT;
-  FERRET_HIP_CHECK((set_lds_limit_once<fp8_square_kernel>(sq::kLds)));
-  hipLaunchKernelGGL(fp8_square_kernel, dim3(p.n_blocks * p.m_blocks), dim3(sq::kThreads), sq::kLds, st, p);
+  FERRET_HIP_CHECK((set_lds_limit_once<fp8_square_kernel<false>>(sq::kLds)));
+  hipLaunchKernelGGL(fp8_square_kernel<false>, dim3(p.n_blocks * p.m_blocks), dim3(sq::kThreads), sq::kLds, st, p);
+  return (int)hipGetLastError();
+}
+
+// The same with UE8M0 scales in the reference's packed layout (ue8m0.hip),
+// folded into the widening; the dispatch rule is ferret_fp8_square_takes.
+int ferret_fp8_gemm_square_ue8m0(const void* a, const uint32_t* sfa, const void* b, const uint32_t* sfb, void* c,
+                                 int M, int N, int K, hipStream_t st) {
+  sq::Args p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.sfa = sfa;
+  p.b = static_cast<const uint8_t*>(b);
+  p.sfb = sfb;
+  p.out = static_cast<uint16_t*>(c);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.n_blocks = N / sq::kBW;
+  p.m_blocks = (M + sq::kBT - 1) / sq::kBT;
+  FERRET_HIP_CHECK((set_lds_limit_once<fp8_square_kernel<true>>(sq::kLds)));
+  hipLaunchKernelGGL(fp8_square_kernel<true>, dim3(p.n_blocks * p.m_blocks), dim3(sq::kThreads), sq::kLds, st, p);
   return (int)hipGetLastError();
 }

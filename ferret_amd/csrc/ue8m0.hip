@@ -9,7 +9,8 @@
 // with the same per-block products P_kb as the reference's oracle ref_bs
 // (v009:486-505).  The decode is one small HBM-bound pass over the scales into
 // the caller's workspace (M x nk + ceil(N/128) x nk floats), ahead of the GEMM
-// on the same stream.
+// on the same stream.  Shapes of the 256 x 256 kernel skip it: that kernel
+// reads the packed bytes and scales each operand exactly while widening it.
 #include "common.hpp"
 
 namespace ferret {
@@ -60,6 +61,9 @@ size_t ferret_fp8_gemm_ue8m0_workspace(int M, int N, int K) {
 
 extern "C" int ferret_fp8_gemm_blockscale(const void* a, const float* sa, const void* b, const float* sb, void* c,
                                           int M, int N, int K, void* ws, size_t ws_bytes, void* stream);
+bool ferret_fp8_square_takes(int M, int N, int K);
+int ferret_fp8_gemm_square_ue8m0(const void* a, const uint32_t* sfa, const void* b, const uint32_t* sfb, void* c,
+                                 int M, int N, int K, hipStream_t st);
 
 extern "C" int ferret_fp8_gemm_ue8m0(const void* a, const uint32_t* sfa, const void* b, const uint32_t* sfb,
                                      void* c, int M, int N, int K, void* ws, size_t ws_bytes, void* stream) {
@@ -69,6 +73,11 @@ extern "C" int ferret_fp8_gemm_ue8m0(const void* a, const uint32_t* sfa, const v
   FERRET_REQUIRE(M <= 16 || N % 128 == 0, FERRET_ERR_SHAPE);
   const size_t need = ferret_fp8_gemm_ue8m0_workspace(M, N, K);
   FERRET_REQUIRE(ws != nullptr && ws_bytes >= need, FERRET_ERR_WORKSPACE);
+  // Shapes of the 256 x 256 kernel take the packed bytes directly: each
+  // power-of-two scale is applied while its operand is widened to bf16 (no
+  // decode pass, no running rescale).
+  if (M > 16 && ferret_fp8_square_takes(M, N, K))
+    return ferret_fp8_gemm_square_ue8m0(a, sfa, b, sfb, c, M, N, K, (hipStream_t)stream);
   const int nk = K / 128, nbk = (N + 127) / 128;
   uint8_t* base = static_cast<uint8_t*>(ws);
   float* sa = reinterpret_cast<float*>(base);
