@@ -67,6 +67,7 @@ FAMILIES = {
     "kimi_tp8": ["kimi_w4a16_w13_T8_tp8"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0", "quant_act", "moe_combine")
+INT4_LAYOUT = "tiled"  # --int4-layout
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(
     FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
@@ -90,6 +91,10 @@ class Runner:
         self.wl, self.torch, self.ops, self.W = wl, torch, ops, W
         t0 = time.perf_counter()
         self.inp = W.make_inputs(wl, "cuda")
+        if wl.kind == "moe_w4a16" and INT4_LAYOUT == "tiled":
+            # One-time load-time regrouping into 16-row x 128-K tiles (untimed,
+            # as the reference repacks into Marlin's layout before timing).
+            self.inp["wt"] = ops.int4_tile_weights(self.inp["w"])
         self.copies = [self.inp]
         if wl.kind in DENSE_KINDS:
             wbytes = sum(t.numel() * t.element_size() for t in self.inp.values())
@@ -142,7 +147,7 @@ class Runner:
         elif wl.kind == "moe_combine":
             ops.moe_combine(c["o"], c["w"], out=o)
         else:
-            ops.moe_w13_w4a16(c["x"], c["w"], c["ws"], self.rt, out=o)
+            ops.moe_w13_w4a16(c["x"], c.get("wt", c["w"]), c["ws"], self.rt, out=o)
 
     def step(self, i: int, ev=None):
         """One pass of the hot path; `ev` = (start, end) events bracket the GEMM."""
@@ -484,6 +489,7 @@ def driver_mode(args) -> int:
                      "achieved": rf["achieved"], "unit": u2, "frac": rf["frac"],
                      "frac_attainable": rf["frac_attainable"], "bound": rf["bound"],
                      **({"frac_bf16_peak": rf["frac_bf16_peak"]} if "frac_bf16_peak" in rf else {}),
+                     **({"int4_layout": INT4_LAYOUT} if w2.kind == "moe_w4a16" else {}),
                      "oracle_check": chk, **t2})
         correct_all = correct_all and chk["correct"]
         del r2
@@ -517,6 +523,8 @@ def config_of(wl, runner) -> dict:
             c[k] = v
     if runner.n_hit:
         c["experts_hit"] = runner.n_hit
+    if wl.kind == "moe_w4a16":
+        c["int4_layout"] = INT4_LAYOUT
     return c
 
 
@@ -594,7 +602,12 @@ def main(argv=None) -> int:
                     help="only launch the workload's GEMM N times (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",
                     help="only run 3 device copies of B bytes (calibrates FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--int4-layout", choices=("tiled", "checkpoint"), default="tiled",
+                    help="INT4 w13 weights: regrouped once into 16-row x 128-K tiles (default) or the "
+                         "checkpoint's [E, N, K/8] words")
     args = ap.parse_args(argv)
+    global INT4_LAYOUT
+    INT4_LAYOUT = args.int4_layout
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the quantized-GEMM path on "
               "one GPU only (no collective or sharded step exists). Run with --gpus 1.", file=sys.stderr)

@@ -59,12 +59,12 @@ static int try_stream(const SkinnyArgs& a_in, int dense_tiles, int max_tiles, hi
                                       grouped, nsplit, grid);
   if (!plan.ok) return 1;
   // INT4 unit scales are copied as 16-byte chunks of the scale rows.
-  if (F == kINT4 && ((reinterpret_cast<uintptr_t>(a_in.w_scale) & 15) != 0 || a_in.K % 256 != 0)) return 1;
+  if (is_int4(F) && ((reinterpret_cast<uintptr_t>(a_in.w_scale) & 15) != 0 || a_in.K % 256 != 0)) return 1;
   SkinnyArgs a = a_in;
   a.units_n = plan.units_n;
   // INT4 keeps at most one unit of scales ahead: ring depth <= KS.
-  constexpr int D2 = (F == kINT4 && D > 2) ? 2 : D;
-  constexpr int D4 = (F == kINT4 && D > 4) ? 4 : D;
+  constexpr int D2 = (is_int4(F) && D > 2) ? 2 : D;
+  constexpr int D4 = (is_int4(F) && D > 4) ? 4 : D;
   switch (plan.ks) {
     case 2: return launch_stream<F, EPI, RB, NW, 2, D2>(a, dense_tiles, grid, st);
     case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, dense_tiles, grid, st);
@@ -360,10 +360,14 @@ int ferret_moe_w2_fp8_skinny(const void* h, const float* sh, const void* w, cons
   return launch_skinny<kFP8, kStore, 1>(a, max_tiles, st);
 }
 
-extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
-                                    const int32_t* sorted_pair, const int32_t* tiles,
-                                    const int32_t* ntiles, int max_tiles, int tile_m, int T, int topk,
-                                    int E, int N, int K, void* out, void* stream) {
+namespace ferret {
+
+// The W4A16 w13 decode over either weight layout (F = kINT4: the checkpoint's
+// [E, N, K/8] words; kINT4T: the same words in 16-row x 128-K tiles).
+template <int F>
+static int moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws, const int32_t* sorted_pair,
+                         const int32_t* tiles, const int32_t* ntiles, int max_tiles, int tile_m, int T, int topk,
+                         int E, int N, int K, void* out, hipStream_t st) {
   FERRET_REQUIRE(x && wq && ws && sorted_pair && tiles && ntiles && out, FERRET_ERR_NULL);
   FERRET_REQUIRE(T >= 1 && topk >= 1 && E >= 1 && max_tiles >= 0, FERRET_ERR_SHAPE);
   FERRET_REQUIRE(tile_m == 16 && N % 32 == 0 && N >= 32 && K % 128 == 0 && K >= 128, FERRET_ERR_SHAPE);
@@ -380,7 +384,56 @@ extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void
   a.K = K;
   a.units_n = N / 32;
   if (max_tiles <= 0) return FERRET_OK;
-  const int rc = try_stream<kINT4, kSilu, 2, 5, 8>(a, 0, max_tiles, (hipStream_t)stream);
+  const int rc = try_stream<F, kSilu, 2, 5, 8>(a, 0, max_tiles, st);
   if (rc != 1) return rc;
-  return launch_skinny<kINT4, kSilu, 2>(a, max_tiles, (hipStream_t)stream);
+  return launch_skinny<F, kSilu, 2>(a, max_tiles, st);
+}
+
+// One thread per 16-byte chunk of the tiled output:
+// out[e][n/16][k/128][n%16][64 B] = the K-step k/128 slice (64 B) of row n.
+__global__ __launch_bounds__(256) void int4_tile_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ t,
+                                                        long long nchunks, int N, int nkb) {
+  const long long row_bytes = (long long)nkb * 64;
+  for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < nchunks; o += (long long)gridDim.x * 256) {
+    const int c = (int)(o & 3);
+    const int row = (int)((o >> 2) & 15);
+    const long long tile = o >> 6;  // (e * N/16 + block) * nkb + k-step
+    const int ks = (int)(tile % nkb);
+    const long long eb = tile / nkb;  // e * N/16 + block: rows 16 * eb .. of the [E * N] row list
+    const u32x4 v = ld_u32x4_stream(w + (eb * 16 + row) * row_bytes + ks * 64 + c * 16);
+    *reinterpret_cast<u32x4*>(t + o * 16) = v;
+  }
+}
+
+}  // namespace ferret
+
+using namespace ferret;
+
+extern "C" int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
+                                    const int32_t* sorted_pair, const int32_t* tiles,
+                                    const int32_t* ntiles, int max_tiles, int tile_m, int T, int topk,
+                                    int E, int N, int K, void* out, void* stream) {
+  return moe_w13_w4a16<kINT4>(x, wq, ws, sorted_pair, tiles, ntiles, max_tiles, tile_m, T, topk, E, N, K, out,
+                              (hipStream_t)stream);
+}
+
+extern "C" int ferret_moe_w13_w4a16_tiled(const void* x, const void* wq_tiled, const void* ws,
+                                          const int32_t* sorted_pair, const int32_t* tiles,
+                                          const int32_t* ntiles, int max_tiles, int tile_m, int T, int topk,
+                                          int E, int N, int K, void* out, void* stream) {
+  return moe_w13_w4a16<kINT4T>(x, static_cast<const int32_t*>(wq_tiled), ws, sorted_pair, tiles, ntiles,
+                               max_tiles, tile_m, T, topk, E, N, K, out, (hipStream_t)stream);
+}
+
+extern "C" int ferret_int4_tile_weights(const int32_t* wq, void* wq_tiled, int E, int N, int K, void* stream) {
+  FERRET_REQUIRE(wq && wq_tiled, FERRET_ERR_NULL);
+  FERRET_REQUIRE(E >= 1 && N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0, FERRET_ERR_SHAPE);
+  const long long bytes = (long long)E * N * (K / 2);
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(wq);
+  uint8_t* dst = static_cast<uint8_t*>(wq_tiled);
+  FERRET_REQUIRE(dst + bytes <= src || src + bytes <= dst, FERRET_ERR_SHAPE);  // out of place only
+  const long long nchunks = bytes / 16;
+  const unsigned grid = (unsigned)std::min<long long>((nchunks + 255) / 256, 65536);
+  hipLaunchKernelGGL(int4_tile_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, dst, nchunks, N, K / 128);
+  return (int)hipGetLastError();
 }

@@ -5,11 +5,15 @@
 
 namespace ferret {
 
-enum WFmt : int { kBF16 = 0, kFP8 = 1, kINT4 = 2 };
+// kINT4T: the INT4 weights of kINT4 regrouped into 16-row x 128-K tiles, each
+// one contiguous KB (ferret_int4_tile_weights); only the addressing differs.
+enum WFmt : int { kBF16 = 0, kFP8 = 1, kINT4 = 2, kINT4T = 3 };
 enum EpiKind : int { kStore = 0, kSilu = 1 };
 
+constexpr bool is_int4(int f) { return f == kINT4 || f == kINT4T; }
+
 struct SkinnyArgs {
-  const uint8_t* w;         // bf16 / e4m3 [G, N, K] or int32 [G, N, K/8]
+  const uint8_t* w;         // bf16 / e4m3 [G, N, K] or int32 [G, N, K/8]; kINT4T: [G, N/16, K/128, 16, 64 B]
   const void* w_scale;      // FP8: f32 [G, N/128, K/128]; INT4: bf16 [G, N, K/32]
   const uint8_t* x;         // bf16 / e4m3 [T, K]
   const float* x_scale;     // FP8: f32 [T, K/128]
@@ -44,6 +48,8 @@ struct FmtTraits<kINT4> {
   static constexpr int kWVec = 1;
   static constexpr int kXVec = 4;
 };
+template <>
+struct FmtTraits<kINT4T> : FmtTraits<kINT4> {};
 
 constexpr int kRedStride = 17;              // padded token stride in the LDS reduction
 constexpr int kRedBlock = 16 * kRedStride;  // floats per (wave, row block)
@@ -133,10 +139,14 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
     else
       rowb[rb] = (nu * RB + rb) * 16;
   }
+  // This lane's weight row at K-step 0; a K-step advances it by ks_bytes.
+  // kINT4T: row r of the block's first 1-KB tile.
   const uint8_t* wrow[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
-    wrow[rb] = a.w + ((size_t)e * N + rowb[rb] + r) * row_bytes;
+    wrow[rb] = F == kINT4T ? a.w + ((size_t)e * (N >> 4) + (rowb[rb] >> 4)) * (size_t)nkb * 1024 + r * 64
+                           : a.w + ((size_t)e * N + rowb[rb] + r) * row_bytes;
+  const size_t ks_bytes = F == kINT4T ? 1024 : 64;  // INT4 forms only
   const uint8_t* xrow = a.x + (size_t)tok * (F == kFP8 ? (size_t)K : (size_t)K * 2);
 
   const int ks0 = wave * KS;
@@ -173,7 +183,7 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
       const uint16_t* sp = static_cast<const uint16_t*>(a.w_scale);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        wbuf[slot][rb][0] = ld_u32x4_stream(wrow[rb] + (size_t)ks * 64 + 16 * g);
+        wbuf[slot][rb][0] = ld_u32x4_stream(wrow[rb] + (size_t)ks * ks_bytes + 16 * g);
         s4[slot][rb] = sp[((size_t)e * N + rowb[rb] + r) * (size_t)(K >> 5) + ks * 4 + g];
       }
 #pragma unroll

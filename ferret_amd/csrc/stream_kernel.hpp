@@ -10,7 +10,9 @@
 //
 // Data movement.  Weights go global -> LDS with global_load_lds_dwordx4
 // (no VGPR staging) into a ring of D stages private to each wave; every bf16 /
-// FP8 DMA instruction reads complete 128-byte lines (8 lanes per line).  A wave waits
+// FP8 DMA instruction reads complete 128-byte lines (8 lanes per line), a
+// tiled-INT4 (kINT4T) one a contiguous KB, and a checkpoint-layout INT4 one
+// 16 half lines (64 B of each of 16 rows).  A wave waits
 // only for its own copies (vmcnt), so the main loop has no barrier, and the
 // ring runs ahead across unit boundaries.  LDS rows keep their 16-byte chunks
 // XOR-swizzled so the MFMA fragment reads are free of bank conflicts.  The
@@ -47,6 +49,8 @@ struct StreamFmt<kINT4> {
   static constexpr int kRowB = 64;
   static constexpr int kInstr = 1;
 };
+template <>
+struct StreamFmt<kINT4T> : StreamFmt<kINT4> {};
 
 template <int F, int RB, int NW, int KS, int D>
 struct StreamCfg {
@@ -67,12 +71,12 @@ struct StreamCfg {
   // stride of 64 B would pile 8 rows onto each of two groups.
   static constexpr int kSclCh = ((KS * 8 + 8 + 15) / 16) | 1;
   static constexpr int kSclBuf = RB * 16 * kSclCh * 16;
-  static constexpr int kSclLoads = F == kINT4 ? (RB * 16 * kSclCh + 63) / 64 : 0;
-  static constexpr int kScl = F == kINT4 ? 2 * kSclBuf : 0;            // per wave
+  static constexpr int kSclLoads = is_int4(F) ? (RB * 16 * kSclCh + 63) / 64 : 0;
+  static constexpr int kScl = is_int4(F) ? 2 * kSclBuf : 0;            // per wave
   static constexpr int kRed = NW * RB * kRedBlock * 4;                // one reduction buffer
   static constexpr int kTiles = kStreamMaxTiles * 3 * 4;              // grouped tile table
   static constexpr int kLds = NW * (kRing + kScl) + 2 * kRed + kTiles;
-  static_assert(F != kINT4 || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
+  static_assert(!is_int4(F) || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
   static_assert(kLds <= 160 * 1024, "LDS budget");
   // Step s reads the fragments of step s + 1 before refilling, so item s + 1
   // must already be in flight: at least two stages per wave.
@@ -245,7 +249,8 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     if constexpr (F == kBF16) c = sw_bf16(row, slot);
     else if constexpr (F == kFP8) c = sw_fp8(row, slot);
     else c = sw_int4(row, slot);
-    lane_off[i] = (uint32_t)row * (uint32_t)wrow_bytes + c * 16;
+    // kINT4T: the 16 rows x 64 B of a block's K-step are one contiguous KB.
+    lane_off[i] = (uint32_t)row * (F == kINT4T ? 64u : (uint32_t)wrow_bytes) + c * 16;
   }
   int iu = u_begin, is = 0;
   const uint8_t* ibase[RB];
@@ -265,8 +270,10 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
     const int e = tile_expert(tile);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
-      ibase[rb] = a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)kstep0 * ROWB;
-    if constexpr (F == kINT4) {
+      ibase[rb] = F == kINT4T
+                      ? a.w + (((size_t)e * (N >> 4) + (block_row(nu, rb) >> 4)) * nkb + kstep0) * (size_t)1024
+                      : a.w + ((size_t)e * N + block_row(nu, rb)) * wrow_bytes + (size_t)kstep0 * ROWB;
+    if constexpr (is_int4(F)) {
 #pragma unroll
       for (int q = 0; q < SI; ++q) {
         const int idx = q * 64 + lane, row = idx / SCH, ch = idx % SCH;
@@ -284,19 +291,21 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   };
   auto issue = [&](int slot) {
     uint8_t* st = ring + slot * C::kStage;
-    // Weight rows are streamed once: non-temporal, except INT4, whose 64-byte
-    // row slice per K-step is half a line -- the other half is the wave's next
-    // K-step and must still be in L2 when it is read.
+    // Weight rows are streamed once: non-temporal, except checkpoint-layout
+    // INT4, whose 64-byte row slice per K-step is half a line -- the other half
+    // is the wave's next K-step and must still be in L2 when it is read.  A
+    // kINT4T op reads one whole KB (its tile: 8 complete lines).
+    constexpr size_t kStepB = F == kINT4T ? 1024 : ROWB;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const uint8_t* src = ibase[rb] + (size_t)is * ROWB + lane_off[i];
+        const uint8_t* src = ibase[rb] + (size_t)is * kStepB + lane_off[i];
         if constexpr (F == kINT4) g2l_16(src, st + (rb * NI + i) * 1024);
         else g2l_16_nt(src, st + (rb * NI + i) * 1024);
       }
     if constexpr (F == kFP8) g2l_4(isc + is * 4, st + C::kWBytes);
-    if constexpr (F == kINT4) {
+    if constexpr (is_int4(F)) {
       if (is == 0) {
         uint8_t* sb = sclbuf + (iu & 1) * C::kSclBuf;
 #pragma unroll

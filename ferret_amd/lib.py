@@ -32,6 +32,9 @@ SIGNATURES = {
                                     _c_int, _c_int, _vp, _vp]),
     "ferret_moe_w13_w4a16": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _vp, _vp]),
+    "ferret_moe_w13_w4a16_tiled": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                            _c_int, _c_int, _c_int, _vp, _vp]),
+    "ferret_int4_tile_weights": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "ferret_quant_act_e4m3": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
     "ferret_moe_w2_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _vp, _vp]),

@@ -300,12 +300,45 @@ def moe_w13_fp8(x: torch.Tensor, sx: torch.Tensor, w: torch.Tensor, sw: torch.Te
     return out
 
 
+def int4_tile_weights(wq: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The INT4 w13 weights wq [E, N, K/8] int32 regrouped into 16-row x 128-K
+    tiles: int32 [E, N/16, K/128, 16, 16], tile (e, b, k) = the 64 bytes of
+    K-step k of rows 16b .. 16b+15 of expert e.  A one-time load-time
+    permutation of the checkpoint words (no value changes); moe_w13_w4a16 on
+    the result streams each tile as one contiguous KB."""
+    _dev(wq, "wq", torch.int32, 3)
+    E, N, K8 = wq.shape
+    K = K8 * 8
+    if N % 16 != 0 or K % 128 != 0:
+        raise ValueError("int4_tile_weights needs N % 16 == 0 and K % 128 == 0")
+    _same_device(wq, out)
+    shape = (E, N // 16, K // 128, 16, 16)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.int32, device=wq.device)
+    rc = _lib.load().ferret_int4_tile_weights(wq.data_ptr(), _out(out, "out", shape, torch.int32, wq.device),
+                                              E, N, K, _stream())
+    _lib.check("ferret_int4_tile_weights", rc)
+    return out
+
+
 def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: Routing,
                   out: torch.Tensor | None = None) -> torch.Tensor:
-    """out[P, N/2] bf16 = silu(gate) * up of the INT4 W4A16 w13 projection."""
+    """out[P, N/2] bf16 = silu(gate) * up of the INT4 W4A16 w13 projection.
+    wq: the checkpoint words int32 [E, N, K/8], or their tiles from
+    int4_tile_weights (int32 [E, N/16, K/128, 16, 16]); the result is the same
+    bit for bit."""
     T, K = x.shape
-    E, N, K8 = wq.shape
-    if K8 * 8 != K or E != routing.num_experts or T != routing.num_tokens:
+    tiled = wq.dim() == 5
+    if tiled:
+        E, NB, KB, R, C = wq.shape
+        if (R, C) != (16, 16) or KB * 128 != K:
+            raise ValueError("tiled wq must be [E, N/16, K/128, 16, 16] int32")
+        N = NB * 16
+    else:
+        E, N, K8 = wq.shape
+        if K8 * 8 != K:
+            raise ValueError("shape mismatch between x and wq")
+    if E != routing.num_experts or T != routing.num_tokens:
         raise ValueError("shape mismatch between x, wq and routing")
     if tuple(ws.shape) != (E, N, K // 32):
         raise ValueError("ws must be [E, N, K/32] bf16")
@@ -314,11 +347,13 @@ def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, routing: 
     if out is None:
         out = torch.empty((P, N // 2), dtype=torch.bfloat16, device=x.device)
     _out(out, "out", (P, N // 2), torch.bfloat16, x.device)
-    rc = _lib.load().ferret_moe_w13_w4a16(
-        _dev(x, "x", torch.bfloat16, 2), _dev(wq, "wq", torch.int32, 3), _dev(ws, "ws", torch.bfloat16, 3),
-        routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(), routing.ntiles.data_ptr(), routing.max_tiles,
-        routing.tile_m, T, routing.topk, E, N, K, _dev(out, "out", torch.bfloat16, 2), _stream())
-    _lib.check("ferret_moe_w13_w4a16", rc)
+    lib = _lib.load()
+    fn, name = ((lib.ferret_moe_w13_w4a16_tiled, "ferret_moe_w13_w4a16_tiled") if tiled
+                else (lib.ferret_moe_w13_w4a16, "ferret_moe_w13_w4a16"))
+    rc = fn(_dev(x, "x", torch.bfloat16, 2), _dev(wq, "wq", torch.int32, wq.dim()), _dev(ws, "ws", torch.bfloat16, 3),
+            routing.sorted_pair.data_ptr(), routing.tiles.data_ptr(), routing.ntiles.data_ptr(), routing.max_tiles,
+            routing.tile_m, T, routing.topk, E, N, K, _dev(out, "out", torch.bfloat16, 2), _stream())
+    _lib.check(name, rc)
     return out
 
 

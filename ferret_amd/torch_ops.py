@@ -145,7 +145,20 @@ def moe_w13_w4a16(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, sorted_pa
 
 @moe_w13_w4a16.register_fake
 def _(x, wq, ws, sorted_pair, tiles, ntiles, tile_m, topk):
-    return x.new_empty((x.shape[0] * topk, wq.shape[1] // 2), dtype=torch.bfloat16)
+    n = wq.shape[1] * 16 if wq.dim() == 5 else wq.shape[1]  # tiled [E, N/16, K/128, 16, 16] or [E, N, K/8]
+    return x.new_empty((x.shape[0] * topk, n // 2), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::int4_tile_weights", mutates_args=())
+def int4_tile_weights(wq: torch.Tensor) -> torch.Tensor:
+    """INT4 w13 words [E, N, K/8] int32 -> 16-row x 128-K tiles [E, N/16, K/128, 16, 16] int32."""
+    return _ops.int4_tile_weights(wq)
+
+
+@int4_tile_weights.register_fake
+def _(wq):
+    E, N, K8 = wq.shape
+    return wq.new_empty((E, N // 16, K8 // 16, 16, 16), dtype=torch.int32)
 
 
 @torch.library.custom_op(f"{_NS}::moe_w2_fp8", mutates_args=())
@@ -173,4 +186,4 @@ def _(o, weights):
 
 
 OPS = ("linear_bf16", "fp8_gemm_blockscale", "fp8_gemm_ue8m0", "quant_act_e4m3", "moe_route_topk", "moe_permute",
-       "moe_w13_fp8", "moe_w13_w4a16", "moe_w2_fp8", "moe_combine")
+       "moe_w13_fp8", "moe_w13_w4a16", "int4_tile_weights", "moe_w2_fp8", "moe_combine")

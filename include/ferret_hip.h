@@ -189,6 +189,32 @@ int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
                          void* out, void* stream);
 
 /*
+ * One-time load-time regrouping of the INT4 w13 words for
+ * ferret_moe_w13_w4a16_tiled: wq int32 [E,N,K/8] -> wq_tiled [E][N/16][K/128]
+ * tiles of 16 rows x 64 bytes (the rows' K-step slices, bytes unchanged),
+ * each tile one contiguous KB.  Out of place (overlapping buffers are
+ * rejected).  Replaces the load-time weight permutation the reference runs
+ * before its GEMM, ops.gptq_marlin_moe_repack
+ * (baselines/kimi-moe-w13-int4/baseline_marlin.py:62-89), which the task
+ * contract allows (tasks/kimi-moe-w13-int4-grouped-gemm.yaml:68-71).
+ * Requirements: N % 16 == 0, K % 128 == 0.
+ */
+int ferret_int4_tile_weights(const int32_t* wq, void* wq_tiled, int E, int N, int K, void* stream);
+
+/*
+ * ferret_moe_w13_w4a16 on weights regrouped by ferret_int4_tile_weights: the
+ * same arguments and the same result bit for bit; each weight DMA reads one
+ * contiguous KB instead of 64 bytes of each of 16 rows.  ws stays [E,N,K/32].
+ * Replaces ops.moe_wna16_marlin_gemm on Marlin's permuted weights
+ * (baselines/kimi-moe-w13-int4/baseline_marlin.py:139-168).
+ * Requirements: as ferret_moe_w13_w4a16.
+ */
+int ferret_moe_w13_w4a16_tiled(const void* x, const void* wq_tiled, const void* ws,
+                               const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
+                               int max_tiles, int tile_m, int T, int topk, int E, int N, int K,
+                               void* out, void* stream);
+
+/*
  * 1x128 activation quantizer: bf16 x [M,K] -> OCP e4m3 q [M,K] and fp32
  * scale [M,K/128] with, per 128-element block of a row (fp32, correctly rounded
  * division):  amax = max(|x| over the block, 1e-4);  q = e4m3_RNE(x * (448/amax));

@@ -15,7 +15,8 @@ Pinned by (tests/test_oracle_formats.py): the 256-code e4m3 table against
 encode against torch's cast on every code midpoint; bf16 against
 ``torch.Tensor.to(torch.bfloat16)`` on random and edge bit patterns; INT4 on the
 known-answer words 0x76543210 / 0xFEDCBA98 and exhaustively over 16 values x 8
-nibble positions.
+nibble positions; the INT4 tile regrouping against an element-by-element loop
+over the contract's description and by its inverse.
 """
 from __future__ import annotations
 
@@ -147,3 +148,24 @@ def int4_dequant_kmajor(raw_q: np.ndarray, scales_bf16_bits: np.ndarray, group: 
     :func:`int4_dequant` on the transposed packing).
     """
     return int4_dequant(np.ascontiguousarray(raw_q.T), np.ascontiguousarray(scales_bf16_bits.T), group)
+
+
+def int4_tile_weights(wq: np.ndarray) -> np.ndarray:
+    """INT4 w13 words ``[E, N, K/8]`` regrouped into 16-row x 128-K tiles
+    ``[E, N/16, K/128, 16, 16]`` (int32): tile ``(e, b, k)`` row ``r`` holds the
+    16 words (64 bytes, K = 128k .. 128k+127) of weight row ``16b + r``.
+
+    A pure permutation of the checkpoint words, the kind of one-time load-time
+    pre-permutation ``tasks/kimi-moe-w13-int4-grouped-gemm.yaml:68-71`` allows
+    (the reference runs ``gptq_marlin_moe_repack`` there,
+    ``baselines/kimi-moe-w13-int4/baseline_marlin.py:62-89``).
+    """
+    E, N, K8 = wq.shape
+    assert N % 16 == 0 and K8 % 16 == 0
+    return np.ascontiguousarray(wq.reshape(E, N // 16, 16, K8 // 16, 16).transpose(0, 1, 3, 2, 4))
+
+
+def int4_untile_weights(t: np.ndarray) -> np.ndarray:
+    """Inverse of :func:`int4_tile_weights`."""
+    E, NB, KB, R, C = t.shape
+    return np.ascontiguousarray(t.transpose(0, 1, 3, 2, 4).reshape(E, NB * R, KB * C))

@@ -110,3 +110,44 @@ def test_ue8m0_gemm_rejects_before_launch():
     assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4096, 7168, None, 0, None) == -3
     assert L.ferret_fp8_gemm_ue8m0(1, 1, 1, 1, 1, 256, 4096, 7168, 1, need - 1, None) == -3
     assert L.ferret_workspace_bytes(5, 256, 4096, 7100, 0) == 0
+
+
+def test_int4_tiled_entries_reject_before_launch():
+    """ferret_int4_tile_weights and ferret_moe_w13_w4a16_tiled check pointers,
+    shapes and (tiling) buffer overlap on the host and return before any HIP
+    call (the pointers here are never dereferenced)."""
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    L = lib.load()
+    assert L.ferret_int4_tile_weights(None, 1, 1, 16, 128, None) == -1
+    assert L.ferret_int4_tile_weights(1, None, 1, 16, 128, None) == -1
+    assert L.ferret_int4_tile_weights(1 << 20, 1 << 24, 1, 24, 128, None) == -2     # N % 16
+    assert L.ferret_int4_tile_weights(1 << 20, 1 << 24, 1, 16, 200, None) == -2     # K % 128
+    assert L.ferret_int4_tile_weights(1 << 20, 1 << 24, 0, 16, 128, None) == -2     # E
+    # [1, 16, 128] is 1 KB: destinations inside it (or covering it) are rejected
+    assert L.ferret_int4_tile_weights(1 << 20, (1 << 20) + 16, 1, 16, 128, None) == -2
+    assert L.ferret_int4_tile_weights((1 << 20) + 16, 1 << 20, 1, 16, 128, None) == -2
+    assert L.ferret_int4_tile_weights(1 << 20, 1 << 20, 1, 16, 128, None) == -2
+    assert L.ferret_moe_w13_w4a16_tiled(1, None, 1, 1, 1, 1, 10, 16, 4, 8, 16, 64, 256, 1, None) == -1
+    assert L.ferret_moe_w13_w4a16_tiled(1, 1, 1, 1, 1, 1, 10, 128, 4, 8, 16, 64, 256, 1, None) == -2  # tile_m
+    assert L.ferret_moe_w13_w4a16_tiled(1, 1, 1, 1, 1, 1, 10, 16, 4, 8, 16, 48, 256, 1, None) == -2   # N % 32
+    assert L.ferret_moe_w13_w4a16_tiled(1, 1, 1, 1, 1, 1, 10, 16, 4, 8, 16, 64, 200, 1, None) == -2   # K % 128
+
+
+def test_int4_tiled_python_wrappers_check_before_launch():
+    import torch
+    from ferret_amd import ops
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.int4_tile_weights(torch.zeros((2, 32, 32), dtype=torch.int32))
+    x = torch.zeros((4, 256), dtype=torch.bfloat16)
+    r = ops.Routing(counts=None, offsets=None, sorted_pair=torch.zeros(8, dtype=torch.int32),
+                    tiles=torch.zeros((4, 3), dtype=torch.int32), ntiles=torch.zeros(1, dtype=torch.int32),
+                    tile_m=16, max_tiles=4, num_experts=2, topk=2, num_tokens=4)
+    ws = torch.zeros((2, 64, 8), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="tiled wq"):
+        ops.moe_w13_w4a16(x, torch.zeros((2, 4, 2, 16, 8), dtype=torch.int32), ws, r)
+    with pytest.raises(ValueError, match="tiled wq"):
+        ops.moe_w13_w4a16(x, torch.zeros((2, 4, 3, 16, 16), dtype=torch.int32), ws, r)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.moe_w13_w4a16(x, torch.zeros((2, 4, 2, 16, 16), dtype=torch.int32), ws, r)

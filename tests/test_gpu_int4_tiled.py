@@ -1,0 +1,96 @@
+"""GPU parity of the tiled INT4 weight layout: ferret_int4_tile_weights against
+the oracle's regrouping, and ferret_moe_w13_w4a16_tiled against the
+checkpoint-layout entry point (bit for bit: both stage the same bytes in LDS
+and run the same arithmetic) and against the oracle.
+
+Cases reach both kernels: the stream kernel (K % 256 == 0: the Kimi-K2 decode
+and TP8 rank at full size, a small grouped shape) and the per-unit kernel
+(K % 256 != 0), including its ragged last wave (K/128 = 19)."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as FM
+from oracle import gemm as G
+from tests.gpu_helpers import assert_gemm_close, bf16_out, bits16
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ops(hip):
+    from ferret_amd import ops as O
+    return O
+
+
+def _same(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("E,N,K", [(1, 16, 128), (3, 64, 512), (2, 96, 2432)])
+def test_int4_tile_weights_matches_oracle(ops, E, N, K):
+    _say(f"int4_tile_weights E={E} N={N} K={K}")
+    g = torch.Generator(device="cuda").manual_seed(E * 1000 + N + K)
+    wq = torch.randint(-2 ** 31, 2 ** 31, (E, N, K // 8), generator=g, device="cuda", dtype=torch.int32)
+    t = ops.int4_tile_weights(wq)
+    torch.cuda.synchronize()
+    assert np.array_equal(t.cpu().numpy(), FM.int4_tile_weights(wq.cpu().numpy()))
+
+
+def test_int4_tile_weights_full_size_sampled_experts(ops):
+    """Kimi-K2 w13 (384 experts, N = 4096, K = 7168): experts 0, 1, 191 and 383
+    of the tiled tensor against the oracle's regrouping of the same experts."""
+    from ferret_amd import workloads as W
+    wl = W.WORKLOADS["kimi_w4a16_w13_decode"]
+    _say("int4_tile_weights full size")
+    inp = W.make_inputs(wl, "cuda")
+    t = ops.int4_tile_weights(inp["w"])
+    torch.cuda.synchronize()
+    for e in (0, 1, 191, 383):
+        assert np.array_equal(t[e:e + 1].cpu().numpy(), FM.int4_tile_weights(inp["w"][e:e + 1].cpu().numpy()))
+
+
+@pytest.mark.parametrize("key", ["kimi_w4a16_w13_decode", "kimi_w4a16_w13_T8_tp8"])
+def test_tiled_decode_bit_identical_full_size(ops, key):
+    """The bench workloads: the tiled path equals the checkpoint-layout path
+    (itself checked against the oracle at this size in test_gpu_parity)."""
+    from ferret_amd import workloads as W
+    wl = W.WORKLOADS[key]
+    _say(f"moe_w13_w4a16_tiled full size {key}")
+    inp = W.make_inputs(wl, "cuda")
+    ids, _ = ops.moe_route_topk(inp["logits"], wl.topk)
+    rt = ops.moe_permute(ids, wl.E)
+    ref = ops.moe_w13_w4a16(inp["x"], inp["w"], inp["ws"], rt)
+    t = ops.int4_tile_weights(inp["w"])
+    out = torch.full_like(ref, float("nan"))
+    ops.moe_w13_w4a16(inp["x"], t, inp["ws"], rt, out=out)
+    torch.cuda.synchronize()
+    assert _same(out, ref)
+
+
+@pytest.mark.parametrize("T,E,N,K,topk", [(24, 8, 256, 2048, 2),    # stream kernel
+                                          (33, 5, 256, 896, 2),     # per-unit kernel, one wave of 7 K-steps
+                                          (16, 6, 128, 2432, 3),    # per-unit kernel, ragged last wave
+                                          (9, 4, 512, 7168, 4)])    # stream kernel, Kimi K
+def test_tiled_decode_small_against_oracle(ops, T, E, N, K, topk):
+    _say(f"moe_w13_w4a16_tiled T={T} E={E} N={N} K={K} topk={topk}")
+    g = torch.Generator(device="cuda").manual_seed(T * 7 + E + N + K)
+    x = torch.randn((T, K), generator=g, device="cuda").to(torch.bfloat16)
+    wq = torch.randint(-2 ** 31, 2 ** 31, (E, N, K // 8), generator=g, device="cuda", dtype=torch.int32)
+    ws = (torch.randn((E, N, K // 32), generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+    ids, _ = ops.moe_route_topk(torch.randn((T, E), generator=g, device="cuda"), topk)
+    rt = ops.moe_permute(ids, E, 16)
+    t = ops.int4_tile_weights(wq)
+    out = ops.moe_w13_w4a16(x, t, ws, rt)
+    base = ops.moe_w13_w4a16(x, wq, ws, rt)
+    torch.cuda.synchronize()
+    assert _same(out, base)
+    ref = G.moe_w13_w4a16(bits16(x), wq.cpu().numpy(), bits16(ws), ids.cpu().numpy())
+    assert_gemm_close(bf16_out(out), ref, f"moe_w13_w4a16_tiled K={K}")

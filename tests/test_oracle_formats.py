@@ -123,3 +123,26 @@ def test_int4_dequant_matches_reference_torch_formula():
     ref = (signed * sc).to(torch.bfloat16).to(torch.float32).t().contiguous().numpy()
     ours = F.int4_dequant_kmajor(raw.numpy(), scales.view(torch.int16).numpy().view(np.uint16))
     assert np.array_equal(ref, ours)
+
+
+def test_int4_tile_weights_against_loops_and_inverse():
+    """Tile (e, b, k), row r, word j is word 16k + j of weight row 16b + r of
+    expert e -- checked word by word on a small tensor of distinct values, and
+    the inverse restores the checkpoint words."""
+    E, N, K = 2, 48, 384
+    wq = np.arange(E * N * K // 8, dtype=np.int64).astype(np.int32).reshape(E, N, K // 8)
+    t = F.int4_tile_weights(wq)
+    assert t.shape == (E, N // 16, K // 128, 16, 16)
+    for e in range(E):
+        for b in range(N // 16):
+            for k in range(K // 128):
+                for r in range(16):
+                    for j in range(16):
+                        assert t[e, b, k, r, j] == wq[e, 16 * b + r, 16 * k + j]
+    # the 1-KB tile of (e, b, k) is contiguous in memory
+    flat = t.reshape(-1)
+    off = ((1 * (N // 16) + 2) * (K // 128) + 1) * 256
+    assert np.array_equal(flat[off:off + 256].reshape(16, 16), wq[1, 32:48, 16:32])
+    assert np.array_equal(F.int4_untile_weights(t), wq)
+    rnd = np.random.default_rng(3).integers(-2 ** 31, 2 ** 31, (3, 32, 256 // 8)).astype(np.int32)
+    assert np.array_equal(F.int4_untile_weights(F.int4_tile_weights(rnd)), rnd)

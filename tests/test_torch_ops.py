@@ -56,6 +56,11 @@ def test_fake_shapes_moe():
     o = F.moe_w13_w4a16(m(64, 7168, dtype=bf), m(384, 4096, 896, dtype=i32), m(384, 4096, 224, dtype=bf),
                         m(512, dtype=i32), m(896, 3, dtype=i32), m(1, dtype=i32), 16, 8)
     assert o.shape == (512, 2048)
+    t4 = F.int4_tile_weights(m(384, 4096, 896, dtype=i32))
+    assert t4.shape == (384, 256, 56, 16, 16) and t4.dtype == i32
+    o = F.moe_w13_w4a16(m(64, 7168, dtype=bf), t4, m(384, 4096, 224, dtype=bf),
+                        m(512, dtype=i32), m(896, 3, dtype=i32), m(1, dtype=i32), 16, 8)
+    assert o.shape == (512, 2048)
     o2 = F.moe_w2_fp8(m(32768, 2048, dtype=f8), m(32768, 16), m(256, 7168, 2048, dtype=f8), m(256, 56, 16),
                       sp, tiles, nt, 128, 8)
     assert o2.shape == (32768, 7168)
