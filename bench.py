@@ -17,6 +17,10 @@ per-launch time is used and both are reported).  `cpu_baseline` checks the GPU
 result against the numpy oracle on a bounded sample of the workload and times
 the PyTorch-CPU fp32 dequantize-then-matmul path on that sample with the host's
 physical cores; every `also` workload carries the same oracle check.
+`roofline.traffic` (HBM bytes per launch of the dominant kernel) is measured
+in the run: rocprofv3 FETCH_SIZE / WRITE_SIZE counters over four short child
+runs, calibrated on a device copy of known size (`--traffic committed` reports
+the figure in profiles/traffic.json instead, as do the `also` workloads).
 
 Ferret scoring mode (the reference's KERNEL_RESULT protocol, task_spec.py:277-356):
 
@@ -204,17 +208,74 @@ TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZ
                   "KEY --launch-only 3`, scaled by a copy kernel of known size (not measured in this run)")
 
 
-def traffic_of(key: str):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, if any."""
+def _traffic_record(key: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as fh:
-            rec = json.load(fh).get(key)
+            return json.load(fh).get(key)
     except (OSError, ValueError):
         return None
-    if not rec:
+
+
+def traffic_of(key: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, if any."""
+    rec = _traffic_record(key)
+    return rec.get("bytes_per_launch") if rec else None
+
+
+def measure_traffic(key: str, timeout_s: float = 150.0):
+    """HBM bytes per launch of the workload's dominant kernel (its name as in
+    profiles/traffic.json), measured now: four child runs under rocprofv3, one
+    counter each -- FETCH_SIZE and WRITE_SIZE of `bench.py --workload KEY
+    --launch-only 3`, then of a 256 MiB device copy, whose known size turns the
+    KiB counts into bytes.  Each run starts in /tmp (TMPDIR=/tmp) in its own
+    process group, which is killed if the run outlives timeout_s.  Returns None
+    when rocprofv3 is missing or a pass yields no dispatch of the kernel."""
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+    from ferret_amd import profiling as P
+
+    rec = _traffic_record(key)
+    if not rec or not rec.get("kernel") or shutil.which("rocprofv3") is None:
         return None
-    return rec.get("bytes_per_launch")
+    if "rocprof" in os.environ.get("LD_PRELOAD", "") or any(k.startswith("ROCPROF") for k in os.environ):
+        log("[bench] already under rocprofv3: reporting the committed traffic figure")
+        return None
+    copy_bytes = 256 << 20
+    tmp = tempfile.mkdtemp(prefix="ferret_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    dirs = {}
+    try:
+        for tag, extra in (("w", ["--workload", key, "--launch-only", "3"]),
+                           ("copy", ["--copy-bytes", str(copy_bytes)])):
+            for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+                out = os.path.join(tmp, f"{tag}_{counter}")
+                cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
+                       sys.executable, os.path.join(ROOT, "bench.py"), *extra]
+                log(f"[bench] traffic pass: rocprofv3 --pmc {counter} -- bench.py {' '.join(extra)}")
+                proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                                        stderr=subprocess.DEVNULL, start_new_session=True)
+                try:
+                    proc.wait(timeout=timeout_s)
+                except subprocess.TimeoutExpired:
+                    os.killpg(proc.pid, signal.SIGKILL)
+                    proc.wait()
+                    log(f"[bench] traffic pass {counter} timed out; reporting the committed figure")
+                    return None
+                # rocprofv3 may exit non-zero after the program finished with its CSV written;
+                # the parse below decides.
+                dirs[(tag, counter)] = out
+        t = P.traffic(rec["kernel"], dirs[("w", "FETCH_SIZE")], dirs[("w", "WRITE_SIZE")],
+                      dirs[("copy", "FETCH_SIZE")], dirs[("copy", "WRITE_SIZE")], copy_bytes)
+    except (OSError, ValueError, IndexError, KeyError) as e:
+        log(f"[bench] traffic measurement failed ({e}); reporting the committed figure")
+        return None
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    t["kernel"] = rec["kernel"]
+    return t
 
 
 # ---------------------------------------------------------------------------- CPU oracle leg
@@ -475,6 +536,16 @@ def driver_mode(args) -> int:
     value = per_step / (ms_per_step * 1e-3)
     roof = roofline_of(wl, runner, kernel_ms)
     roof.update(timing)
+    if args.traffic == "measure":
+        t = measure_traffic(wl.key)
+        if t is not None:
+            roof["traffic"] = t["bytes_per_launch"]
+            roof["traffic_source"] = (f"measured in this run: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                                      f"{t['kernel']} (bench.py --workload {wl.key} --launch-only 3), KiB scaled "
+                                      f"by a 256 MiB device copy (factors {t['fetch_factor']} / {t['write_factor']})")
+            roof["traffic_fetch_bytes"], roof["traffic_write_bytes"] = t["fetch_bytes"], t["write_bytes"]
+    if roof.get("traffic"):
+        roof["traffic_ratio"] = round(roof["traffic"] / runner.bytes, 3)
     cpu = None if args.no_cpu_baseline else cpu_baseline(wl, runner, args.cpu_budget)
     also = []
     correct_all = True
@@ -602,6 +673,9 @@ def main(argv=None) -> int:
                     help="only launch the workload's GEMM N times (for hardware-counter runs)")
     ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",
                     help="only run 3 device copies of B bytes (calibrates FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic", choices=("measure", "committed"), default="measure",
+                    help="roofline.traffic of the default workload: measured in this run with rocprofv3 "
+                         "(four short child runs, about a minute) or the committed profiles/traffic.json figure")
     ap.add_argument("--int4-layout", choices=("tiled", "checkpoint"), default="tiled",
                     help="INT4 w13 weights: regrouped once into 16-row x 128-K tiles (default) or the "
                          "checkpoint's [E, N, K/8] words")
