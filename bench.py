@@ -223,7 +223,7 @@ def traffic_of(key: str):
     return rec.get("bytes_per_launch") if rec else None
 
 
-def measure_traffic(key: str, timeout_s: float = 150.0):
+def measure_traffic(key: str, timeout_s: float = 90.0):
     """HBM bytes per launch of the workload's dominant kernel (its name as in
     profiles/traffic.json), measured now: four child runs under rocprofv3, one
     counter each -- FETCH_SIZE and WRITE_SIZE of `bench.py --workload KEY
