@@ -94,3 +94,27 @@ def test_tiled_decode_small_against_oracle(ops, T, E, N, K, topk):
     assert _same(out, base)
     ref = G.moe_w13_w4a16(bits16(x), wq.cpu().numpy(), bits16(ws), ids.cpu().numpy())
     assert_gemm_close(bf16_out(out), ref, f"moe_w13_w4a16_tiled K={K}")
+
+
+def test_tiled_decode_misaligned_scales_per_unit_path(ops):
+    """Scales 2 bytes past a 16-byte boundary: the stream kernel declines (it
+    copies scale rows as 16-byte chunks) and the per-unit kernel runs on the
+    tiled weights at K % 256 == 0; both layouts agree bit for bit there."""
+    T, E, N, K, topk = 12, 6, 256, 2048, 2
+    _say(f"moe_w13_w4a16_tiled misaligned scales T={T} E={E} N={N} K={K}")
+    g = torch.Generator(device="cuda").manual_seed(4242)
+    x = torch.randn((T, K), generator=g, device="cuda").to(torch.bfloat16)
+    wq = torch.randint(-2 ** 31, 2 ** 31, (E, N, K // 8), generator=g, device="cuda", dtype=torch.int32)
+    ws = (torch.randn((E, N, K // 32), generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+    buf = torch.empty(ws.numel() + 1, dtype=torch.bfloat16, device="cuda")
+    buf[1:] = ws.reshape(-1)
+    ws_mis = buf[1:].view(E, N, K // 32)
+    assert ws_mis.is_contiguous() and ws_mis.data_ptr() % 16 == 2
+    ids, _ = ops.moe_route_topk(torch.randn((T, E), generator=g, device="cuda"), topk)
+    rt = ops.moe_permute(ids, E, 16)
+    out = ops.moe_w13_w4a16(x, ops.int4_tile_weights(wq), ws_mis, rt)
+    base = ops.moe_w13_w4a16(x, wq, ws_mis, rt)
+    torch.cuda.synchronize()
+    assert _same(out, base)
+    ref = G.moe_w13_w4a16(bits16(x), wq.cpu().numpy(), bits16(ws), ids.cpu().numpy())
+    assert_gemm_close(bf16_out(out), ref, "moe_w13_w4a16_tiled misaligned scales")
