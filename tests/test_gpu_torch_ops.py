@@ -54,6 +54,28 @@ def test_opcheck_routing(T):
     torch.library.opcheck(F.moe_permute.default, (ids, 32, 16))
 
 
+def test_opcheck_int4(T):
+    """int4_tile_weights and moe_w13_w4a16 on both weight layouts: schemas and
+    fake shapes against the kernels; the two layouts give the same bits."""
+    _say("opcheck int4 ops")
+    F = torch.ops.ferret
+    g = torch.Generator(device="cuda").manual_seed(31)
+    Tn, E, N, K, topk = 8, 6, 128, 1024, 2
+    x = torch.randn((Tn, K), generator=g, device="cuda").to(torch.bfloat16)
+    wq = torch.randint(-2 ** 31, 2 ** 31, (E, N, K // 8), generator=g, device="cuda", dtype=torch.int32)
+    ws = (torch.randn((E, N, K // 32), generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+    ids, _ = F.moe_route_topk(torch.randn((Tn, E), generator=g, device="cuda"), topk)
+    counts, offsets, sp, tiles, nt = F.moe_permute(ids, E, 16)
+    torch.library.opcheck(F.int4_tile_weights.default, (wq,))
+    wt = F.int4_tile_weights(wq)
+    for w in (wq, wt):
+        torch.library.opcheck(F.moe_w13_w4a16.default, (x, w, ws, sp, tiles, nt, 16, topk))
+    a = F.moe_w13_w4a16(x, wq, ws, sp, tiles, nt, 16, topk)
+    b = F.moe_w13_w4a16(x, wt, ws, sp, tiles, nt, 16, topk)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def _moe_inputs(Tn=48, E=8, N=512, K=1024, topk=2, seed=7):
     from ferret_amd import workloads as W
     g = torch.Generator(device="cuda")
