@@ -78,7 +78,9 @@ def test_tiled_decode_bit_identical_full_size(ops, key):
 @pytest.mark.parametrize("T,E,N,K,topk", [(24, 8, 256, 2048, 2),    # stream kernel
                                           (33, 5, 256, 896, 2),     # per-unit kernel, one wave of 7 K-steps
                                           (16, 6, 128, 2432, 3),    # per-unit kernel, ragged last wave
-                                          (9, 4, 512, 7168, 4)])    # stream kernel, Kimi K
+                                          (9, 4, 512, 7168, 4),     # stream kernel, Kimi K
+                                          (1, 1, 32, 128, 1),       # one K-step, one wave
+                                          (5, 3, 64, 256, 1)])      # two K-steps: the stream plan declines
 def test_tiled_decode_small_against_oracle(ops, T, E, N, K, topk):
     _say(f"moe_w13_w4a16_tiled T={T} E={E} N={N} K={K} topk={topk}")
     g = torch.Generator(device="cuda").manual_seed(T * 7 + E + N + K)
