@@ -392,7 +392,7 @@ static int moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws, const
 // One thread per 16-byte chunk of the tiled output:
 // out[e][n/16][k/128][n%16][64 B] = the K-step k/128 slice (64 B) of row n.
 __global__ __launch_bounds__(256) void int4_tile_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ t,
-                                                        long long nchunks, int N, int nkb) {
+                                                        long long nchunks, int nkb) {
   const long long row_bytes = (long long)nkb * 64;
   for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < nchunks; o += (long long)gridDim.x * 256) {
     const int c = (int)(o & 3);
@@ -434,6 +434,6 @@ extern "C" int ferret_int4_tile_weights(const int32_t* wq, void* wq_tiled, int E
   FERRET_REQUIRE(dst + bytes <= src || src + bytes <= dst, FERRET_ERR_SHAPE);  // out of place only
   const long long nchunks = bytes / 16;
   const unsigned grid = (unsigned)std::min<long long>((nchunks + 255) / 256, 65536);
-  hipLaunchKernelGGL(int4_tile_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, dst, nchunks, N, K / 128);
+  hipLaunchKernelGGL(int4_tile_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, dst, nchunks, K / 128);
   return (int)hipGetLastError();
 }
