@@ -58,6 +58,44 @@ def _compile(src: str, verbose: bool) -> tuple[str, str]:
     return obj, out
 
 
+def resource_usage(sources=None, jobs: int | None = None) -> dict[str, dict[str, int]]:
+    """Per-kernel register, scratch and LDS use of the device code, from hipcc's
+    kernel-resource-usage remarks (a device-only compile into a scratch
+    directory; the library is not touched).  Returns {mangled name: {"vgpr",
+    "agpr", "sgpr", "scratch" (bytes per lane), "vgpr_spill", "sgpr_spill",
+    "occupancy" (waves per SIMD), "lds" (static bytes)}}."""
+    import re
+    import tempfile
+
+    fields = {"VGPRs": "vgpr", "AGPRs": "agpr", "TotalSGPRs": "sgpr", "ScratchSize [bytes/lane]": "scratch",
+              "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill", "Occupancy [waves/SIMD]": "occupancy",
+              "LDS Size [bytes/block]": "lds"}
+    keys = sorted(fields, key=len, reverse=True)  # "VGPRs Spill" before "VGPRs"
+    pat = re.compile(r"remark:\s+(Function Name|" + "|".join(re.escape(k) for k in keys) + r"): (\S+)")
+
+    def one(src: str, tmp: str) -> str:
+        cmd = [hipcc(), *HIPCC_FLAGS, "--offload-device-only", "-c", os.path.join(CSRC, src), "-o",
+               os.path.join(tmp, src + ".o"), "-Rpass-analysis=kernel-resource-usage"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}{res.stderr}")
+        return res.stderr
+
+    out: dict[str, dict[str, int]] = {}
+    srcs = list(sources or SOURCES)
+    with tempfile.TemporaryDirectory() as tmp, \
+            cf.ThreadPoolExecutor(max_workers=jobs or min(len(srcs), os.cpu_count() or 1)) as ex:
+        for text in ex.map(lambda s: one(s, tmp), srcs):
+            cur = None
+            for m in pat.finditer(text):
+                key, val = m.group(1), m.group(2)
+                if key == "Function Name":
+                    cur = out.setdefault(val, {})
+                elif cur is not None:
+                    cur[fields[key]] = int(val)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:

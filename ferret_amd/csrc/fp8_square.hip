@@ -28,11 +28,14 @@
 // is one VALU multiply per accumulator and block, as a separate fold would
 // be, but with no partial-sum registers, which is what lets a wave hold a
 // 128 x 64 tile in its 256 VGPRs.  r carries one extra fp32 rounding per
-// block (~56 * 2^-24 relative at K = 7168).  A block whose scale product is 0
+// block (~56 * 2^-24 relative at K = 7168); r comes from the reciprocal of s
+// while every s of the wave lies in [2^-125, 2^125], else from an IEEE
+// division (subnormal products included).  A block whose scale product is 0
 // keeps the unit and has its token fragments cleared in the lanes of those
-// columns, so it adds nothing.  Precondition (every quantizer of this library
-// meets it): scales are finite, a product sa * sb is either 0 or a normal
-// float, and |C| / s stays inside the fp32 range for each block scale s.
+// columns, so it adds nothing.  Precondition: scales are finite, and the
+// block sums in units of each block's s stay inside the fp32 range -- with
+// |a b| <= 448^2 per product that holds while the non-zero products sa * sb of
+// one output span less than 2^90.
 //
 // Schedule.  The work of a stage is pinned to its 32 MFMA slots (see the
 // stage lambda): fragment reads one substep ahead, the widening and LDS
@@ -164,26 +167,32 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
   const int wkey = swz_key(lrow);  // the same for rows lrow + 16 i
   const int wch0 = ((2 * q) ^ wkey) << 4, wch1 = ((2 * q + 1) ^ wkey) << 4;
 
-  // UE8M0 mode: the scale word of each loaded row (4 K-blocks per byte
-  // word), fetched with the row's stage bytes; a weight row reads the word of
-  // its 128-row block.  Words past the arrays read as 0.
+  // UE8M0 mode: the scale word of each loaded row (4 K-blocks per byte word),
+  // fetched with the stage bytes: lane q of each lane quad loads the word of
+  // part q (row lrow + 16 q; a weight row reads the word of its 128-row block,
+  // the same for every part) and write_part(i) takes part i's word from lane
+  // i of the quad (DPP), one register per stage in flight instead of four.
+  // The whole offset goes in voffset, which the buffer range check covers:
+  // words past the array read as 0.
   const int nsk = (nkb + 3) >> 2;
   const __amdgpu_buffer_rsrc_t sf_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(U8 ? (loads_tokens ? p.sfa : p.sfb) : nullptr), (short)0,
       U8 ? nsk * (loads_tokens ? p.M : p.N) * 4 : 0, 0x00020000);
   const int sf_ld = loads_tokens ? p.M : p.N;  // words per sk row
-  const int sf_row0 = loads_tokens ? tok0 + lrow : wrow0 + (lrow & ~127);  // + 16 i (tokens)
+  const int sf_row = loads_tokens ? tok0 + lrow + 16 * q : wrow0 + (lrow & ~127);
 
   // Two stages in flight in registers (stg[st & 1]): the L2 / MALL latency
   // under load is longer than one stage's compute.
   u32x4 stg[2][4];
-  uint32_t sfw[2][4];
+  uint32_t sfw[2];
   auto load_part = [&](int st, int i) {
     stg[st & 1][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
         rsrc, (int)(loff + (unsigned)(16 * i * K)), st * kKS, 0));
     if constexpr (U8) {
-      const int row = sf_row0 + (loads_tokens ? 16 * i : 0);
-      sfw[st & 1][i] = __builtin_amdgcn_raw_buffer_load_b32(sf_rsrc, row * 4, (st >> 3) * sf_ld * 4, 0);
+      // with the last part: load_part(st, i) follows write_part(st - 2, i),
+      // so the register is refilled only after all four parts of stage st - 2
+      // have taken their word from it
+      if (i == 3) sfw[st & 1] = __builtin_amdgcn_raw_buffer_load_b32(sf_rsrc, (sf_row + (st >> 3) * sf_ld) * 4, 0, 0);
     }
   };
   auto write_part = [&](int st, int i) {
@@ -192,7 +201,16 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
     if constexpr (U8) {
       // byte of K-block st / 2; a zero byte is a zero scale (the instruction
       // would take it as 2^-127), so its values are cleared instead
-      const uint32_t e = (sfw[st & 1][i] >> (8 * ((st >> 1) & 3))) & 0xFFu;
+      // quad_perm [i, i, i, i]: the word lane i of the quad loaded
+      const int wsrc = (int)sfw[st & 1];
+      int word;
+      switch (i) {
+        case 0: word = __builtin_amdgcn_mov_dpp(wsrc, 0x00, 0xF, 0xF, false); break;
+        case 1: word = __builtin_amdgcn_mov_dpp(wsrc, 0x55, 0xF, 0xF, false); break;
+        case 2: word = __builtin_amdgcn_mov_dpp(wsrc, 0xAA, 0xF, 0xF, false); break;
+        default: word = __builtin_amdgcn_mov_dpp(wsrc, 0xFF, 0xF, 0xF, false); break;
+      }
+      const uint32_t e = ((uint32_t)word >> (8 * ((st >> 1) & 3))) & 0xFFu;
       const float sc = __uint_as_float(e << 23);
       const uint32_t m = e != 0 ? 0xFFFFFFFFu : 0u;
       *reinterpret_cast<bf16x8*>(row + wch0) = e4m3x8_to_bf16x8_scaled(v[0] & m, v[1] & m, sc);
@@ -204,15 +222,14 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
   };
 
   // ---- scales.  Token scales of the lane's 2 token columns
-  // (tbase + 32 mi + c32), one K block ahead, by buffer loads (columns past M
-  // read as 0 and are never stored); weight-block scales of the wave's 128
-  // rows in lanes (lane l: blocks l and 64 + l), picked per block with
-  // v_readlane.
+  // (tbase + 32 mi + c32), one K block ahead, by buffer loads with the whole
+  // offset in voffset (the range check covers it: columns past M read as 0
+  // and are never stored); weight-block scales of the wave's 128 rows in
+  // lanes (lane l: blocks l and 64 + l), picked per block with v_readlane.
   const __amdgpu_buffer_rsrc_t sa_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.sa + (size_t)tok0 * nkb), (short)0, tok_rows * nkb * 4, 0x00020000);
-  const int sa_off = (tbase + c32) * nkb * 4;  // + 32 mi rows + 4 kb
   auto load_sa = [&](int mi, int kb) {
-    return __builtin_amdgcn_raw_buffer_load_b32(sa_rsrc, sa_off, (32 * mi * nkb + kb) * 4, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(sa_rsrc, ((tbase + 32 * mi + c32) * nkb + kb) * 4, 0, 0);
   };
   float sb_lo = 0.f, sb_hi = 0.f;
   float sa_nx[kMI] = {};
@@ -242,12 +259,24 @@ __global__ __launch_bounds__(sq::kThreads) void fp8_square_kernel(sq::Args p) {
     const float sbv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
         __builtin_bit_cast(int, kb < 64 ? sb_lo : sb_hi), kb & 63));
     zm_nx = 0;
+    float s[kMI];
+    bool extreme = false;
 #pragma unroll
     for (int mi = 0; mi < kMI; ++mi) {
-      const float s = sa_nx[mi] * sbv;
-      const bool live = s != 0.f;
-      rs[mi] = (live && unit[mi] != 0.f) ? unit[mi] * __builtin_amdgcn_rcpf(s) : 1.f;
-      unit[mi] = live ? s : unit[mi];
+      s[mi] = sa_nx[mi] * sbv;
+      const float a = __builtin_fabsf(s[mi]);
+      extreme |= a != 0.f && !(a >= 0x1p-125f && a <= 0x1p125f);  // NaN / inf count too
+    }
+    // rs = unit / s: by the reciprocal while every s of the wave lies in
+    // [2^-125, 2^125] (its reciprocal is then a normal float), else by IEEE
+    // division, so subnormal scale products are handled as the fp32 oracle does.
+    const bool exact_div = __builtin_amdgcn_ballot_w64(extreme) != 0;  // wave-uniform
+#pragma unroll
+    for (int mi = 0; mi < kMI; ++mi) {
+      const bool live = s[mi] != 0.f;
+      const float r = exact_div ? unit[mi] / s[mi] : unit[mi] * __builtin_amdgcn_rcpf(s[mi]);
+      rs[mi] = (live && unit[mi] != 0.f) ? r : 1.f;
+      unit[mi] = live ? s[mi] : unit[mi];
       zm_nx |= live ? 0u : 1u << mi;
     }
   };

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
     } else {
       const int row = (j - C::kWInstr) * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ swz_key(row);
-      const int t = min(row, nrows - 1);
+      const int t = max(0, min(row, nrows - 1));  // rows past the tile repeat its last row (a zero-row tile: row0)
       const int tok = GROUPED ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
       goff[i] = (size_t)tok * K + chunk * 16;
     }
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
   const bool sa_wave = wave >= TB_WAVES - 2;
   const float* sa_src = nullptr;
   if (sa_wave) {
-    const int t = min((wave - (TB_WAVES - 2)) * 64 + lane, nrows - 1);
+    const int t = max(0, min((wave - (TB_WAVES - 2)) * 64 + lane, nrows - 1));
     const int tok = GROUPED ? p.sorted_pair[row0 + t] / p.topk : row0 + t;
     sa_src = p.sa + (size_t)tok * nkb;
   }

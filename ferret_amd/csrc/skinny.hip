@@ -62,14 +62,18 @@ static int try_stream(const SkinnyArgs& a_in, int dense_tiles, int max_tiles, hi
   if (is_int4(F) && ((reinterpret_cast<uintptr_t>(a_in.w_scale) & 15) != 0 || a_in.K % 256 != 0)) return 1;
   SkinnyArgs a = a_in;
   a.units_n = plan.units_n;
+  const int slots = grouped ? max_tiles : dense_tiles;
   // INT4 keeps at most one unit of scales ahead: ring depth <= KS.
   constexpr int D2 = (is_int4(F) && D > 2) ? 2 : D;
   constexpr int D4 = (is_int4(F) && D > 4) ? 4 : D;
   switch (plan.ks) {
-    case 2: return launch_stream<F, EPI, RB, NW, 2, D2>(a, dense_tiles, grid, st);
-    case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, dense_tiles, grid, st);
-    case 7: return launch_stream<F, EPI, RB, NW, 7, D>(a, dense_tiles, grid, st);
-    case 8: return launch_stream<F, EPI, RB, NW, 8, D>(a, dense_tiles, grid, st);
+    case 2: return launch_stream<F, EPI, RB, NW, 2, D2>(a, slots, grid, st);
+    case 4: return launch_stream<F, EPI, RB, NW, 4, D4>(a, slots, grid, st);
+    // More than 8 waves leave a wave 128 VGPRs (two work-groups' worth of waves
+    // on some SIMDs), too few for 7 or 8 K-steps of activations: those shapes
+    // take the 8-wave configuration (the caller's fallback).
+    case 7: if constexpr (NW <= 8) return launch_stream<F, EPI, RB, NW, 7, D>(a, slots, grid, st); else return 1;
+    case 8: if constexpr (NW <= 8) return launch_stream<F, EPI, RB, NW, 8, D>(a, slots, grid, st); else return 1;
   }
   return 1;
 }
@@ -97,6 +101,11 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
   if (grid <= 0) return FERRET_OK;
   // Prefetch depth kept so a wave stays within 128 VGPRs (16 waves / CU).
   constexpr int DB = (F == kBF16) ? 2 : ((F == kFP8 && RB == 1) ? 4 : (F == kFP8 ? 3 : 2));
+  // 7 or 8 K-steps per wave hold more activations: FP8 row pairs (SiLU) keep a
+  // 2-deep prefetch and the ragged single-block form a 3-deep one, or they
+  // spill past 128 VGPRs.
+  constexpr int D78 = (F == kFP8 && RB >= 2) ? 2 : DB;
+  constexpr int D78R = (F == kFP8 && RB == 1) ? 3 : D78;
   if (ks == 0) {
     // No K-step count divides K/128 into <= 16 waves (K/128 = 19, 23, 38, ...):
     // the smallest of 2, 4, 7, 8 that fits 16 waves, the last wave ragged.
@@ -106,8 +115,8 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
       switch (kr) {
         case 2: return launch_one<F, EPI, RB, 2, 1, true>(a, grid, nw, st);
         case 4: return launch_one<F, EPI, RB, 4, (DB < 3 ? DB : 3), true>(a, grid, nw, st);
-        case 7: return launch_one<F, EPI, RB, 7, DB, true>(a, grid, nw, st);
-        case 8: return launch_one<F, EPI, RB, 8, DB, true>(a, grid, nw, st);
+        case 7: return launch_one<F, EPI, RB, 7, D78R, true>(a, grid, nw, st);
+        case 8: return launch_one<F, EPI, RB, 8, D78R, true>(a, grid, nw, st);
       }
     }
     return FERRET_ERR_SHAPE;  // K/128 > 128: rejected by every entry point first
@@ -117,8 +126,8 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
     case 1: return launch_one<F, EPI, RB, 1, 0>(a, grid, nwaves, st);
     case 2: return launch_one<F, EPI, RB, 2, 1>(a, grid, nwaves, st);
     case 4: return launch_one<F, EPI, RB, 4, (DB < 3 ? DB : 3)>(a, grid, nwaves, st);
-    case 7: return launch_one<F, EPI, RB, 7, DB>(a, grid, nwaves, st);
-    case 8: return launch_one<F, EPI, RB, 8, DB>(a, grid, nwaves, st);
+    case 7: return launch_one<F, EPI, RB, 7, D78>(a, grid, nwaves, st);
+    case 8: return launch_one<F, EPI, RB, 8, D78>(a, grid, nwaves, st);
   }
   return FERRET_ERR_SHAPE;
 }
@@ -256,7 +265,14 @@ static hipError_t scratch_address(void** out) {
   return hipSuccess;
 }
 
-extern "C" size_t ferret_linear_bf16_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+// Also looks the array's address up on the current device (errors are left
+// for the entry point to report), so that a caller can do it before capturing
+// ferret_linear_bf16_noalloc into a graph.
+extern "C" size_t ferret_linear_bf16_noalloc_max_bytes(void) {
+  void* p = nullptr;
+  (void)scratch_address(&p);
+  return kNoAllocScratchBytes;
+}
 
 extern "C" int ferret_linear_bf16_noalloc(const void* x, const void* w, const void* residual, void* y, int M,
                                           int N, int K, void* stream) {

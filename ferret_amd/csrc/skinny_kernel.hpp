@@ -124,7 +124,8 @@ __global__ __launch_bounds__(1024) void skinny_gemm_kernel(SkinnyArgs a) {
     row0 = tile_idx * 16;
     nrows = min(16, a.M - row0);
   }
-  const int tcol = min(r, nrows - 1);  // clamp: columns >= nrows compute garbage, never stored
+  // clamp: columns >= nrows compute garbage, never stored (a zero-row tile reads row row0)
+  const int tcol = max(0, min(r, nrows - 1));
   const int tok = grouped ? a.sorted_pair[row0 + tcol] / a.topk : row0 + tcol;
 
   const int N = a.N, K = a.K;

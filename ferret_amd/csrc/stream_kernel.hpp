@@ -75,7 +75,15 @@ struct StreamCfg {
   static constexpr int kScl = is_int4(F) ? 2 * kSclBuf : 0;            // per wave
   static constexpr int kRed = NW * RB * kRedBlock * 4;                // one reduction buffer
   static constexpr int kTiles = kStreamMaxTiles * 3 * 4;              // grouped tile table
-  static constexpr int kLds = NW * (kRing + kScl) + 2 * kRed + kTiles;
+  // LDS layout, in this order: each wave's ring and INT4 scale buffers, the
+  // two reduction buffers, the tile table (the kernel takes every offset from
+  // here).
+  static constexpr int kWaveBytes = kRing + kScl;
+  static constexpr int kRedOff = NW * kWaveBytes;
+  static constexpr int kTileOff = kRedOff + 2 * kRed;
+  static constexpr int kLds = kTileOff + kTiles;
+  static_assert(kRedOff % 16 == 0 && kTileOff % 16 == 0, "LDS regions 16-byte aligned");
+  static_assert(kTileOff + kStreamMaxTiles * 3 * (int)sizeof(int) == kLds, "the tile table ends the LDS");
   static_assert(!is_int4(F) || D <= KS, "INT4 unit scales are double-buffered: at most one unit ahead");
   static_assert(kLds <= 160 * 1024, "LDS budget");
   // Step s reads the fragments of step s + 1 before refilling, so item s + 1
@@ -177,8 +185,10 @@ struct StepFrag {
   float sv[RB];
 };
 
+// tile_slots: dense, the token tiles of M; grouped, the rows of the tile table
+// (max_tiles), which bounds the device-side count a.ntiles[0].
 template <int F, int EPI, int RB, int NW, int KS, int D>
-__global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int dense_tiles) {
+__global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int tile_slots) {
   using C = StreamCfg<F, RB, NW, KS, D>;
   constexpr int ROWB = StreamFmt<F>::kRowB;
   constexpr int NI = StreamFmt<F>::kInstr;
@@ -203,7 +213,9 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   const size_t wrow_bytes = (size_t)K * ROWB / 128;
 
   // ---- this work-group's units
-  const int ntiles = grouped ? __builtin_amdgcn_readfirstlane(a.ntiles[0]) : dense_tiles;
+  // The grouped count is clamped to the table's rows: the host's launch plan
+  // (units per work-group, the LDS span of the table) assumes ntiles <= max_tiles.
+  const int ntiles = grouped ? min(max(__builtin_amdgcn_readfirstlane(a.ntiles[0]), 0), tile_slots) : tile_slots;
   // bf16 dense split-K: work item u = split * (ntiles * units_n) + unit; the
   // item's waves cover K-steps [(split * NW + w) * KS, ... + KS).
   const int nsplit = (F == kBF16 && !grouped && a.partial != nullptr) ? a.ksplit : 1;
@@ -215,10 +227,10 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
   const int n_items = (u_end - u_begin) * KS;
   if (n_items == 0) return;
 
-  uint8_t* ring = lds + wave * (C::kRing + C::kScl);
+  uint8_t* ring = lds + wave * C::kWaveBytes;
   uint8_t* sclbuf = ring + C::kRing;  // INT4 unit scales (two buffers)
-  float* red = reinterpret_cast<float*>(lds + NW * (C::kRing + C::kScl));
-  int* tinfo = reinterpret_cast<int*>(lds + NW * (C::kRing + C::kScl) + 2 * C::kRed);
+  float* red = reinterpret_cast<float*>(lds + C::kRedOff);
+  int* tinfo = reinterpret_cast<int*>(lds + C::kTileOff);
 
   // Grouped: copy this work-group's rows of the tile table to LDS once, so the
   // loop reads them without vector-memory loads (which would drain the ring).
@@ -340,7 +352,8 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
       row0 = tile * 16;
       nrows = min(16, a.M - row0);
     }
-    const int tcol = min(r, nrows - 1);  // columns >= nrows compute garbage, never stored
+    // columns >= nrows compute garbage, never stored (a zero-row tile reads row row0)
+    const int tcol = max(0, min(r, nrows - 1));
     tok = row0 + tcol;
     if (grouped) {
       my_pair = a.sorted_pair[row0 + tcol];
@@ -580,11 +593,11 @@ __global__ __launch_bounds__(NW * 64) void stream_gemm_kernel(SkinnyArgs a, int 
 }
 
 template <int F, int EPI, int RB, int NW, int KS, int D>
-static int launch_stream(const SkinnyArgs& a, int dense_tiles, int grid, hipStream_t st) {
+static int launch_stream(const SkinnyArgs& a, int tile_slots, int grid, hipStream_t st) {
   using C = StreamCfg<F, RB, NW, KS, D>;
   FERRET_HIP_CHECK((set_lds_limit_once<stream_gemm_kernel<F, EPI, RB, NW, KS, D>>(C::kLds)));
   hipLaunchKernelGGL((stream_gemm_kernel<F, EPI, RB, NW, KS, D>), dim3(grid), dim3(NW * 64), C::kLds, st, a,
-                     dense_tiles);
+                     tile_slots);
   return (int)hipGetLastError();
 }
 

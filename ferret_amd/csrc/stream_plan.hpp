@@ -39,6 +39,8 @@ inline StreamPlan stream_plan(bool silu, int rb, int nw, int N, int K, int tiles
   if (nkb % (nw * nsplit) != 0) return p;
   p.ks = nkb / nsplit / nw;
   if (p.ks != 2 && p.ks != 4 && p.ks != 7 && p.ks != 8) return p;
+  // Past 8 waves a wave has 128 VGPRs: at most 4 K-steps of activations.
+  if (nw > 8 && p.ks > 4) return p;
   p.nsplit = nsplit;
   p.units = (long long)tiles * p.units_n * nsplit;
   p.per = (p.units + grid - 1) / grid;

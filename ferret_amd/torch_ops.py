@@ -95,8 +95,23 @@ def _(logits, topk):
     return logits.new_empty((T, topk), dtype=torch.int32), logits.new_empty((T, topk), dtype=torch.float32)
 
 
-def _tile_m(num_pairs: int, num_experts: int, tile_m: int) -> int:
-    return tile_m if tile_m > 0 else int(_lib.load().ferret_moe_tile_m(num_pairs, num_experts))
+def moe_tile_m(num_pairs, num_experts: int):
+    """ferret_moe_tile_m (routing.hip) in Python, so that fake tensors and
+    symbolic pair counts need no library call: 128-row tiles from an average
+    of 32 rows per expert, else 16."""
+    return 128 if num_experts > 0 and num_pairs // num_experts >= 32 else 16
+
+
+def moe_max_tiles(num_pairs, num_experts: int, tile_m: int):
+    """ferret_moe_max_tiles (routing.hip) in Python: min(ceil(P / tile_m) + E, P),
+    0 without pairs; works on SymInts (torch.sym_min)."""
+    if num_pairs <= 0 or tile_m <= 0:
+        return 0
+    return torch.sym_min((num_pairs + tile_m - 1) // tile_m + num_experts, num_pairs)
+
+
+def _tile_m(num_pairs, num_experts: int, tile_m: int):
+    return tile_m if tile_m > 0 else moe_tile_m(num_pairs, num_experts)
 
 
 @torch.library.custom_op(f"{_NS}::moe_permute", mutates_args=())
@@ -114,10 +129,11 @@ def moe_permute(ids: torch.Tensor, num_experts: int, tile_m: int = 0) -> tuple[t
 def _(ids, num_experts, tile_m=0):
     P = ids.shape[0] * ids.shape[1]
     tm = _tile_m(P, num_experts, tile_m)
-    max_tiles = max(1, int(_lib.load().ferret_moe_max_tiles(P, num_experts, tm)))
+    max_tiles = torch.sym_max(1, moe_max_tiles(P, num_experts, tm))
     i32 = dict(dtype=torch.int32)
     return (ids.new_empty((num_experts,), **i32), ids.new_empty((num_experts + 1,), **i32),
-            ids.new_empty((max(P, 1),), **i32), ids.new_empty((max_tiles, 3), **i32), ids.new_empty((1,), **i32))
+            ids.new_empty((torch.sym_max(P, 1),), **i32), ids.new_empty((max_tiles, 3), **i32),
+            ids.new_empty((1,), **i32))
 
 
 # ---- MoE GEMMs and tail ----------------------------------------------------------------------------

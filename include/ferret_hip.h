@@ -74,12 +74,15 @@ int ferret_linear_bf16(const void* x, const void* w, const void* residual, void*
  * larger than that) is rejected with FERRET_ERR_WORKSPACE.  The result is
  * bit-identical to ferret_linear_bf16 with a workspace.  Calls that overlap on
  * one GPU (different streams or threads) share the array and race: serialise
- * them.  The first call on each device looks the array's address up once.
+ * them.  The array's address is looked up once per device, by the first call
+ * of ferret_linear_bf16_noalloc_max_bytes or of this entry point on it: make
+ * one of them on each device before capturing this entry point into a graph.
  */
 int ferret_linear_bf16_noalloc(const void* x, const void* w, const void* residual, void* y, int M,
                                int N, int K, void* stream);
 
-/* Bytes of the device array ferret_linear_bf16_noalloc uses (its limit). */
+/* Bytes of the device array ferret_linear_bf16_noalloc uses (its limit); also
+ * looks the array's address up on the current device. */
 size_t ferret_linear_bf16_noalloc_max_bytes(void);
 
 /*

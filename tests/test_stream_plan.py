@@ -129,3 +129,34 @@ def test_checker_rejects_the_rb_mismatch_that_faulted(tmp_path):
     exe = _build(tmp_path, "MUTANT_RB_MISMATCH")
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert res.returncode != 0 and "weight row >= N" in res.stdout
+
+
+def _instantiations():
+    """(silu, RB, NW, grouped) of every try_stream<F, EPI, RB, D[, NW]>(a, dense_tiles, max_tiles, st)
+    call in skinny.hip (NW defaults to 8; a call with dense_tiles 0 is grouped)."""
+    import re
+    src = open(os.path.join(CSRC, "skinny.hip")).read()
+    pat = re.compile(r"try_stream<\s*(\w+)\s*,\s*(\w+)\s*,\s*(\d+)\s*,\s*(\d+)\s*(?:,\s*(\d+)\s*)?>\s*"
+                     r"\(\s*a\s*,\s*([^,]+?)\s*,\s*([^,]+?)\s*,\s*st\s*\)")
+    calls = [(m.group(2) == "kSilu", int(m.group(3)), int(m.group(5) or 8), m.group(6) == "0")
+             for m in pat.finditer(src)]
+    return calls, src.count("try_stream<")   # the template's definition is `try_stream(`
+
+
+def _checker_cfgs():
+    import re
+    body = CHECKER[CHECKER.index("kCfgs[] = {"):CHECKER.index("};", CHECKER.index("kCfgs[] = {"))]
+    return {(m.group(1) == "true", int(m.group(2)), int(m.group(3)), m.group(4) == "true")
+            for m in re.finditer(r'\{"[^"]*",\s*(true|false),\s*(\d+),\s*(\d+),\s*(true|false),\s*\d+\}', body)}
+
+
+def test_checker_covers_every_try_stream_instantiation():
+    """kCfgs above is written by hand: every try_stream instantiation in
+    skinny.hip must appear in it, so an added or changed one cannot escape the
+    bounds walk."""
+    calls, n_sites = _instantiations()
+    assert len(calls) == n_sites >= 9, (len(calls), n_sites)   # the regex saw every call site
+    cfgs = _checker_cfgs()
+    assert len(cfgs) >= 6   # distinct (silu, RB, NW, grouped) tuples of the eight entries
+    missing = sorted(set(calls) - cfgs)
+    assert not missing, f"try_stream instantiations not walked by the checker (silu, RB, NW, grouped): {missing}"

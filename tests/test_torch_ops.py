@@ -73,3 +73,45 @@ def test_cpu_tensors_are_refused():
     with pytest.raises(ValueError, match="GPU tensor"):
         torch.ops.ferret.linear_bf16(torch.zeros(1, 128, dtype=torch.bfloat16),
                                      torch.zeros(16, 128, dtype=torch.bfloat16), None)
+
+
+def test_tile_formulas_match_the_library():
+    """The fake implementations size moe_permute's outputs with Python copies of
+    ferret_moe_tile_m / ferret_moe_max_tiles (no library call, SymInt-safe);
+    they must equal the C functions."""
+    T = _ops()
+    L = lib.load()
+    for P in (0, 1, 7, 8, 15, 16, 17, 127, 128, 129, 1000, 1024, 8191, 8192, 32768, 1 << 20):
+        for E in (1, 8, 32, 256, 384, 1024):
+            tm = T.moe_tile_m(P, E)
+            assert tm == L.ferret_moe_tile_m(P, E), (P, E)
+            for tile_m in (1, 16, 128, tm):
+                assert T.moe_max_tiles(P, E, tile_m) == L.ferret_moe_max_tiles(P, E, tile_m), (P, E, tile_m)
+
+
+def test_moe_permute_fake_calls_no_library(monkeypatch):
+    T = _ops()
+
+    def refuse():
+        raise AssertionError("the fake implementation called into libferret_hip.so")
+    monkeypatch.setattr(T._lib, "load", refuse)
+    counts, offsets, sp, tiles, nt = torch.ops.ferret.moe_permute(m(100, 8, dtype=torch.int32), 32, 0)
+    # 800 pairs over 32 experts: 25 rows per expert, 16-row tiles, ceil(800 / 16) + 32 table rows
+    assert sp.shape == (800,) and tiles.shape == (82, 3) and counts.shape == (32,)
+
+
+def test_moe_permute_exports_with_a_dynamic_token_count():
+    """torch.export traces moe_permute with the token count symbolic: the table
+    size comes out as a symbolic expression, not a specialised constant."""
+    _ops()
+
+    class Route(torch.nn.Module):
+        def forward(self, ids):
+            return torch.ops.ferret.moe_permute(ids, 256, 128)
+
+    ids = torch.zeros((4096, 8), dtype=torch.int32)
+    ep = torch.export.export(Route(), (ids,), dynamic_shapes=({0: torch.export.Dim("T", min=2, max=1 << 18)},))
+    outs = [n for n in ep.graph.nodes if n.op == "output"][0].args[0]
+    shapes = [tuple(o.meta["val"].shape) for o in outs]
+    assert shapes[0] == (256,) and shapes[1] == (257,)
+    assert not isinstance(shapes[2][0], int) and not isinstance(shapes[3][0], int), shapes

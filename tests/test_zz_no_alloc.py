@@ -62,3 +62,43 @@ def test_noalloc_rejects_partials_beyond_the_array(hip):
                                       torch.cuda.current_stream().cuda_stream)
     assert rc == -3
     assert L.ferret_error_string(rc).decode().startswith("workspace")
+
+
+def test_noalloc_under_graph_capture(hip):
+    """Captured into a HIP graph (after the address lookup that
+    ferret_linear_bf16_noalloc_max_bytes does), every replay with new inputs is
+    bit-identical to the workspace entry point run eagerly on the same inputs."""
+    from ferret_amd import workloads as W
+    L = hip
+    M, N, K = 16, 6144, 4096                      # splits K: partials in the library's array
+    assert int(L.ferret_workspace_bytes(0, M, N, K, 0)) > 0
+    assert int(L.ferret_linear_bf16_noalloc_max_bytes()) == 4 << 20
+    x = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
+    w = W.randn((N, K), 41, "cuda", std=0.02).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    x.copy_(W.randn((M, K), 40, "cuda").to(torch.bfloat16))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                 # warm-up off the default stream, as capture requires
+        assert L.ferret_linear_bf16_noalloc(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K,
+                                            side.cuda_stream) == 0
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = L.ferret_linear_bf16_noalloc(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K,
+                                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    need = int(L.ferret_workspace_bytes(0, M, N, K, 0))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    ref = torch.empty_like(y)
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        x.copy_(W.randn((M, K), 50 + rep, "cuda").to(torch.bfloat16))
+        y.fill_(-1.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert L.ferret_linear_bf16(x.data_ptr(), w.data_ptr(), None, ref.data_ptr(), M, N, K, ws.data_ptr(),
+                                    need, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {rep} differs"
