@@ -158,6 +158,26 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// Sum, in split order, of the split-K partials of f32x4 element i (splits n4
+// elements apart): S > 0 splits known at compile time, all loads issued before
+// the first add; S == 0 takes the runtime count `splits` one load at a time.
+template <int S>
+__device__ __forceinline__ f32x4 sum_splits(const f32x4* __restrict__ part, int splits, size_t n4, size_t i) {
+  if constexpr (S > 0) {
+    f32x4 v[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) v[s] = part[(size_t)s * n4 + i];
+    f32x4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) acc += v[s];
+    return acc;
+  } else {
+    f32x4 acc = part[i];
+    for (int s = 1; s < splits; ++s) acc += part[(size_t)s * n4 + i];
+    return acc;
+  }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }

@@ -90,12 +90,13 @@ struct TiledArgs {
 __device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * TB_K + ((chunk ^ swz_key(row)) << 4); }
 
-// Sum the split-K fp32 partials in split order (deterministic) and round to bf16.
+// Sum the split-K fp32 partials in split order (deterministic) and round to
+// bf16; S > 0: that many splits, all loaded before the first add.
+template <int S>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, size_t n4,
                                                            uint16_t* __restrict__ out) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-    f32x4 acc = reinterpret_cast<const f32x4*>(part)[i];
-    for (int s = 1; s < splits; ++s) acc += reinterpret_cast<const f32x4*>(part)[(size_t)s * n4 + i];
+    const f32x4 acc = sum_splits<S>(reinterpret_cast<const f32x4*>(part), splits, n4, i);
     u32x2 v;
     v[0] = pack_bf16x2(acc[0], acc[1]);
     v[1] = pack_bf16x2(acc[2], acc[3]);
@@ -516,14 +517,29 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
       }
     }
   } else {
-    // split-K: fp32 partials, 16 B per lane.
+    // split-K: fp32 partials.  As for the bf16 store, the idle ring stages the
+    // wave's TOKW x 64 sub-tile (pitch 272 B: the 16 rows of one write land on
+    // distinct banks), so that each store writes four whole 256-B row segments
+    // instead of 64-B quarters of 16 rows.
+    if (nb * TB_N + wn * 64 >= N) return;  // wave's rows lie past N
+    constexpr int PITCH = 272;
+    static_assert(TB_WAVES * TOKW * PITCH <= C::kLds, "staging fits the ring");
+    uint8_t* stg = lds + wave * TOKW * PITCH;
 #pragma unroll
-    for (int mi = 0; mi < MIX; ++mi) {
-      const int tl = wm * TOKW + mi * 16 + r;  // token row inside the tile
-      if (tl >= nrows || nb * TB_N + wn * 64 >= N) continue;
-      float* o = p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64;
+    for (int mi = 0; mi < MIX; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) *reinterpret_cast<f32x4*>(o + ni * 16 + 4 * g) = acc[ni][mi];
+      for (int ni = 0; ni < 4; ++ni)
+        *reinterpret_cast<f32x4*>(stg + (mi * 16 + r) * PITCH + ni * 64 + g * 16) = acc[ni][mi];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own rows are written
+    const int chunk = lane & 15;
+#pragma unroll
+    for (int it = 0; it < TOKW / 4; ++it) {
+      const int rw = it * 4 + (lane >> 4);
+      const int tl = wm * TOKW + rw;  // token row inside the tile
+      const f32x4 v = *reinterpret_cast<const f32x4*>(stg + rw * PITCH + chunk * 16);
+      if (tl < nrows)
+        *reinterpret_cast<f32x4*>(p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64 +
+                                  chunk * 4) = v;
     }
   }
 }
@@ -597,8 +613,9 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
                                  : launch_tiled<false, false, SPLITK_WN, true, false, SPLITK_TW>(p, grid, st, f8);
     if (rc != 0) return rc;
     const size_t n4 = (size_t)M * N / 4;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(512), dim3(256), 0, st, p.partial, used, n4,
-                       static_cast<uint16_t*>(c));
+    auto* reduce = used == 2 ? splitk_reduce_kernel<2> : used == 4 ? splitk_reduce_kernel<4>
+                 : used == 8 ? splitk_reduce_kernel<8> : splitk_reduce_kernel<0>;
+    hipLaunchKernelGGL(reduce, dim3(512), dim3(256), 0, st, p.partial, used, n4, static_cast<uint16_t*>(c));
     return (int)hipGetLastError();
   }
   // Dense tiles: with every token tile full (M % 128 == 0) the kernel skips

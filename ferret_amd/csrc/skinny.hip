@@ -132,17 +132,14 @@ static int launch_skinny(const SkinnyArgs& a, int ntile_slots, hipStream_t st) {
   return FERRET_ERR_SHAPE;
 }
 
-// y[m, n] = bf16(sum_{s < S} partial[s, m, n] (+ residual[m, n])), splits in order.
+// y[m, n] = bf16(sum_{s < S} partial[s, m, n] (+ residual[m, n])), splits in
+// order; SN > 0: S == SN, all split loads issued before the first add.
+template <int SN>
 __global__ __launch_bounds__(256) void linear_splitk_reduce_kernel(const float* __restrict__ partial, int S,
                                                                    long long mn4, const uint16_t* __restrict__ res,
                                                                    uint16_t* __restrict__ y) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < mn4; i += (long long)gridDim.x * 256) {
-    f32x4 v = reinterpret_cast<const f32x4*>(partial)[i];
-    for (int s = 1; s < S; ++s) {
-      const f32x4 p = reinterpret_cast<const f32x4*>(partial + (size_t)s * mn4 * 4)[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] += p[j];
-    }
+    f32x4 v = sum_splits<SN>(reinterpret_cast<const f32x4*>(partial), S, (size_t)mn4, (size_t)i);
     if (res) {
       const u32x2 r = reinterpret_cast<const u32x2*>(res)[i];
       v[0] += __uint_as_float(r[0] << 16);
@@ -215,8 +212,9 @@ extern "C" int ferret_linear_bf16(const void* x, const void* w, const void* resi
       if (rc != 0) return rc;
       const long long mn4 = (long long)M * N / 4;
       const int grid = (int)std::min<long long>((mn4 + 255) / 256, 4096);
-      hipLaunchKernelGGL(linear_splitk_reduce_kernel, dim3(grid), dim3(256), 0, st, a.partial, splits, mn4,
-                         a.residual, a.out);
+      auto* reduce = splits == 2 ? linear_splitk_reduce_kernel<2> : splits == 3 ? linear_splitk_reduce_kernel<3>
+                   : splits == 4 ? linear_splitk_reduce_kernel<4> : linear_splitk_reduce_kernel<0>;
+      hipLaunchKernelGGL(reduce, dim3(grid), dim3(256), 0, st, a.partial, splits, mn4, a.residual, a.out);
       return (int)hipGetLastError();
     }
     a.partial = nullptr;
