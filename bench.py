@@ -71,6 +71,9 @@ FAMILIES = {
     "kimi_tp8": ["kimi_w4a16_w13_T8_tp8"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0", "quant_act", "moe_combine")
+# `also` workloads measured like the default one (in-run traffic, own CPU
+# baseline): the largest BASELINE configuration, the DSv3 MoE w13 prefill.
+MEASURED_ALSO = ("dsv3_moe_w13_prefill",)
 INT4_LAYOUT = "tiled"  # --int4-layout
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(
@@ -223,14 +226,18 @@ def traffic_of(key: str):
     return rec.get("bytes_per_launch") if rec else None
 
 
+_COPY_FACTORS = None  # (fetch, write) bytes per counted KiB, from the first measurement of a run
+
+
 def measure_traffic(key: str, timeout_s: float = 90.0):
     """HBM bytes per launch of the workload's dominant kernel (its name as in
-    profiles/traffic.json), measured now: four child runs under rocprofv3, one
+    profiles/traffic.json), measured now: child runs under rocprofv3, one
     counter each -- FETCH_SIZE and WRITE_SIZE of `bench.py --workload KEY
-    --launch-only 3`, then of a 256 MiB device copy, whose known size turns the
-    KiB counts into bytes.  Each run starts in /tmp (TMPDIR=/tmp) in its own
-    process group, which is killed if the run outlives timeout_s.  Returns None
-    when rocprofv3 is missing or a pass yields no dispatch of the kernel."""
+    --launch-only 3`, then (once per bench run) of a 256 MiB device copy, whose
+    known size turns the KiB counts into bytes.  Each run starts in /tmp
+    (TMPDIR=/tmp) in its own process group, which is killed if the run outlives
+    timeout_s.  Returns None when rocprofv3 is missing or a pass yields no
+    dispatch of the kernel."""
     import shutil
     import signal
     import subprocess
@@ -247,9 +254,12 @@ def measure_traffic(key: str, timeout_s: float = 90.0):
     tmp = tempfile.mkdtemp(prefix="ferret_pmc_", dir="/tmp")
     env = dict(os.environ, TMPDIR="/tmp")
     dirs = {}
+    global _COPY_FACTORS
+    passes = [("w", ["--workload", key, "--launch-only", "3"])]
+    if _COPY_FACTORS is None:
+        passes.append(("copy", ["--copy-bytes", str(copy_bytes)]))
     try:
-        for tag, extra in (("w", ["--workload", key, "--launch-only", "3"]),
-                           ("copy", ["--copy-bytes", str(copy_bytes)])):
+        for tag, extra in passes:
             for counter in ("FETCH_SIZE", "WRITE_SIZE"):
                 out = os.path.join(tmp, f"{tag}_{counter}")
                 cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
@@ -267,8 +277,10 @@ def measure_traffic(key: str, timeout_s: float = 90.0):
                 # rocprofv3 may exit non-zero after the program finished with its CSV written;
                 # the parse below decides.
                 dirs[(tag, counter)] = out
-        t = P.traffic(rec["kernel"], dirs[("w", "FETCH_SIZE")], dirs[("w", "WRITE_SIZE")],
-                      dirs[("copy", "FETCH_SIZE")], dirs[("copy", "WRITE_SIZE")], copy_bytes)
+        if _COPY_FACTORS is None:
+            _COPY_FACTORS = P.copy_factors(dirs[("copy", "FETCH_SIZE")], dirs[("copy", "WRITE_SIZE")], copy_bytes)
+        t = P.traffic(rec["kernel"], dirs[("w", "FETCH_SIZE")], dirs[("w", "WRITE_SIZE")], "", "", copy_bytes,
+                      factors=_COPY_FACTORS)
     except (OSError, ValueError, IndexError, KeyError) as e:
         log(f"[bench] traffic measurement failed ({e}); reporting the committed figure")
         return None
@@ -555,13 +567,29 @@ def driver_mode(args) -> int:
         m2, k2, t2 = time_steps(r2, max(10, args.steps), 3)
         u2, _ = unit_of(w2)
         rf = roofline_of(w2, r2, k2)
+        entry = {"workload": key, "ms_per_step": round(m2, 5), "kernel_us": rf["kernel_us"],
+                 "achieved": rf["achieved"], "unit": u2, "frac": rf["frac"],
+                 "frac_attainable": rf["frac_attainable"], "bound": rf["bound"],
+                 **({"frac_bf16_peak": rf["frac_bf16_peak"]} if "frac_bf16_peak" in rf else {}),
+                 **({"int4_layout": INT4_LAYOUT} if w2.kind == "moe_w4a16" else {}),
+                 "traffic": rf["traffic"], "traffic_source": "profiles/traffic.json (committed)"}
+        if key in MEASURED_ALSO:
+            # The largest configuration gets the default workload's treatment:
+            # HBM traffic measured in this run and its own CPU baseline.
+            if args.traffic == "measure":
+                t = measure_traffic(key)
+                if t is not None:
+                    entry["traffic"] = t["bytes_per_launch"]
+                    entry["traffic_fetch_bytes"], entry["traffic_write_bytes"] = t["fetch_bytes"], t["write_bytes"]
+                    entry["traffic_source"] = (f"measured in this run: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                                               f"{t['kernel']} (bench.py --workload {key} --launch-only 3)")
+            if not args.no_cpu_baseline:
+                entry["cpu_baseline"] = cpu_baseline(w2, r2, min(args.cpu_budget, 8.0))
+        if entry["traffic"]:
+            entry["traffic_ratio"] = round(entry["traffic"] / r2.bytes, 3)
         chk = oracle_check(w2, r2)
-        also.append({"workload": key, "ms_per_step": round(m2, 5), "kernel_us": rf["kernel_us"],
-                     "achieved": rf["achieved"], "unit": u2, "frac": rf["frac"],
-                     "frac_attainable": rf["frac_attainable"], "bound": rf["bound"],
-                     **({"frac_bf16_peak": rf["frac_bf16_peak"]} if "frac_bf16_peak" in rf else {}),
-                     **({"int4_layout": INT4_LAYOUT} if w2.kind == "moe_w4a16" else {}),
-                     "oracle_check": chk, **t2})
+        entry.update({"oracle_check": chk, **t2})
+        also.append(entry)
         correct_all = correct_all and chk["correct"]
         del r2
     correct = True if cpu is None else cpu["correct"]

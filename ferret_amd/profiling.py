@@ -48,11 +48,18 @@ def counter_per_dispatch(path: str, kernel_substr: str) -> float:
     return statistics.median(vals)
 
 
-def traffic(kernel_substr: str, fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write_dir: str,
-            copy_bytes: int) -> dict:
+def copy_factors(copy_fetch_dir: str, copy_write_dir: str, copy_bytes: int) -> tuple[float, float]:
+    """Bytes per counted KiB of FETCH_SIZE and WRITE_SIZE, from a device copy of copy_bytes."""
     kib = copy_bytes / 1024.0
-    f_factor = kib / counter_per_dispatch(copy_fetch_dir, "copyBuffer")
-    w_factor = kib / counter_per_dispatch(copy_write_dir, "copyBuffer")
+    return (kib / counter_per_dispatch(copy_fetch_dir, "copyBuffer"),
+            kib / counter_per_dispatch(copy_write_dir, "copyBuffer"))
+
+
+def traffic(kernel_substr: str, fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write_dir: str,
+            copy_bytes: int, factors: tuple[float, float] | None = None) -> dict:
+    """HBM bytes per launch of the kernel; `factors` (from copy_factors) skips
+    reading the copy runs again."""
+    f_factor, w_factor = factors or copy_factors(copy_fetch_dir, copy_write_dir, copy_bytes)
     fetch = counter_per_dispatch(fetch_dir, kernel_substr) * f_factor * 1024
     write = counter_per_dispatch(write_dir, kernel_substr) * w_factor * 1024
     return {"fetch_bytes": round(fetch), "write_bytes": round(write), "bytes_per_launch": round(fetch + write),
