@@ -3,6 +3,8 @@
     python -m ferret_amd.profiling trace  <kernel_trace.csv>            # per (kernel, grid) durations
     python -m ferret_amd.profiling traffic <kernel substring> <fetch_dir> <write_dir> \\
         <copy_fetch_dir> <copy_write_dir> <copy_bytes>                  # HBM bytes per launch
+    python -m ferret_amd.profiling counters <kernel substring> <pmc_dir> [<pmc_dir> ...]
+                                                                        # median per dispatch of each counter
 
 FETCH_SIZE / WRITE_SIZE are read in KiB per dispatch and scaled by what the
 same counter reads for a plain device copy of known size (the calibration
@@ -48,6 +50,17 @@ def counter_per_dispatch(path: str, kernel_substr: str) -> float:
     return statistics.median(vals)
 
 
+def counters(kernel_substr: str, path: str) -> dict[str, float]:
+    """Median per dispatch of every counter a rocprofv3 --pmc run recorded for the kernel."""
+    vals = defaultdict(list)
+    for r in _rows(path):
+        if kernel_substr in r["Kernel_Name"]:
+            vals[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    if not vals:
+        raise ValueError(f"no dispatch of {kernel_substr!r} in {path}")
+    return {k: statistics.median(v) for k, v in sorted(vals.items())}
+
+
 def copy_factors(copy_fetch_dir: str, copy_write_dir: str, copy_bytes: int) -> tuple[float, float]:
     """Bytes per counted KiB of FETCH_SIZE and WRITE_SIZE, from a device copy of copy_bytes."""
     kib = copy_bytes / 1024.0
@@ -73,6 +86,12 @@ def main(argv=None) -> int:
         for r in kernel_table(argv[1]):
             print(f"| `{r['kernel'][:90]}` | {r['grid']} | {r['calls']} | {r['avg_us']:.2f} | "
                   f"{r['min_us']:.2f} | {r['max_us']:.2f} |")
+        return 0
+    if argv and argv[0] == "counters":
+        print("| counter | median per dispatch |\n|---|---|")
+        for d in argv[2:]:
+            for name, v in counters(argv[1], d).items():
+                print(f"| {name} | {v:,.0f} |")
         return 0
     if argv and argv[0] == "traffic":
         print(json.dumps(traffic(argv[1], argv[2], argv[3], argv[4], argv[5], int(argv[6]))))

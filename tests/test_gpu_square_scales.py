@@ -39,7 +39,10 @@ def _wide_scales(rng, M, N, K):
     return sa, sb
 
 
-@pytest.mark.parametrize("M,N,K", [(3072, 4096, 1024), (3000, 4096, 1024)])
+# (3072, 4096) and (3000, 4096): 192 square-kernel tiles (the second with a
+# partial last token tile); (1000, 4096): 128 tiles, below the square kernel's
+# threshold, so the 256 x 128 tiled kernel (per-block folds) runs the same check.
+@pytest.mark.parametrize("M,N,K", [(3072, 4096, 1024), (3000, 4096, 1024), (1000, 4096, 1024)])
 def test_square_kernel_scales_over_80_octaves(hip, M, N, K):
     from ferret_amd import ops
     L = hip
