@@ -483,10 +483,16 @@ def time_steps(runner, steps: int, warmup: int):
     (large for a ~10 us kernel), the burst by the gaps between launches --
     so the kernel time is the smaller of the two; both are reported.  The
     burst is enqueued behind a spin kernel, so the host's issue rate does not
-    enter it.
+    enter it.  `board_power_w` is the board's mean power (amdgpu hwmon) over
+    the untimed settle run, which repeats the step back to back for 0.8 s; the
+    first 40 % of its samples (the ramp) are left out.
     """
     import torch
-    settle_clocks(runner)
+    from ferret_amd.power import PowerSampler
+    with PowerSampler(_power_file()) as ps:
+        settle_clocks(runner, 0.8)
+    pw = ps.summary(skip=0.4)
+    power = {"board_power_w": pw["mean_w"] if pw else None}
     for i in range(warmup):
         runner.step(i)
     torch.cuda.synchronize()
@@ -499,7 +505,7 @@ def time_steps(runner, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     pairs_ms = statistics.mean(s.elapsed_time(e) for s, e in evs)
     if runner.wl.kind in MOE_KINDS:
-        return wall * 1e3 / steps, pairs_ms, {"kernel_us_event_pairs": round(pairs_ms * 1e3, 3)}
+        return wall * 1e3 / steps, pairs_ms, {"kernel_us_event_pairs": round(pairs_ms * 1e3, 3), **power}
     # The burst is enqueued while a spin kernel holds the GPU, so the launches
     # run back to back however slowly the host issues them (a ~10 us kernel
     # launches faster than Python can enqueue it).
@@ -516,7 +522,19 @@ def time_steps(runner, steps: int, warmup: int):
     burst_ms = ev0.elapsed_time(ev1) / steps
     return wall * 1e3 / steps, min(pairs_ms, burst_ms), {
         "kernel_us_event_pairs": round(pairs_ms * 1e3, 3), "kernel_us_burst": round(burst_ms * 1e3, 3),
-        "burst_host_enqueue_ms": round(enq_ms, 3)}
+        "burst_host_enqueue_ms": round(enq_ms, 3), **power}
+
+
+_POWER_FILE = []
+
+
+def _power_file():
+    """The device's hwmon board-power file (None where there is none), found once."""
+    if not _POWER_FILE:
+        from ferret_amd.power import pick_power_file, device_pci_bus
+        pick = pick_power_file(device_pci_bus(0))
+        _POWER_FILE.append(pick[1] if pick else None)
+    return _POWER_FILE[0]
 
 
 _SPIN_PER_MS = None
