@@ -75,6 +75,19 @@ DENSE_KINDS = ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0", "quant_act", "moe_co
 # baseline): the largest BASELINE configuration, the DSv3 MoE w13 prefill.
 MEASURED_ALSO = ("dsv3_moe_w13_prefill",)
 INT4_LAYOUT = "tiled"  # --int4-layout
+# The reference's own published figure for a workload of exactly this shape.
+# It comes from other hardware and in another unit than the workload's metric,
+# so it is reported next to the entry as context, never as vs_baseline.
+PUBLISHED = {
+    "qwen3_gateup_M16": {"value": 62.91, "unit": "TFLOP/s", "hardware": "B200",
+                         "what": "the reference's decode kernel (cuBLAS on the same B200: 64.90)",
+                         "source": "tasks/qwen3-8b-decode-linear-bs16-b200.yaml:65"},
+    "kimi_w4a16_w13_T8_tp8": {"value": 13.19, "unit": "TFLOP/s", "hardware": "B200",
+                              "what": "the reference's best INT4 w13 kernel, 128 MB flush before each launch "
+                                      "(vLLM Marlin on the same B200: 9.36)",
+                              "source": "correctness/kimi-moe-w13-precision-fix.md:14, "
+                                        "tasks/kimi-moe-w13-int4-grouped-gemm.yaml:102"},
+}
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(
     FAMILIES["decode_linear"] + FAMILIES["decode_linear_m1"] + FAMILIES["fp8_dense"] + FAMILIES["moe"]
@@ -170,6 +183,15 @@ class Runner:
 
     def output(self):
         return self.outs[0]
+
+
+def published_of(wl, runner, kernel_us: float) -> dict | None:
+    """PUBLISHED's entry for the workload with this run's figure in its unit."""
+    p = PUBLISHED.get(wl.key)
+    if p is None or not kernel_us:
+        return None
+    tflops = runner.flops / (kernel_us * 1e-6) / 1e12
+    return {**p, "this_run": round(tflops, 2), "ratio": round(tflops / p["value"], 3)}
 
 
 def unit_of(wl):
@@ -605,6 +627,9 @@ def driver_mode(args) -> int:
                 entry["cpu_baseline"] = cpu_baseline(w2, r2, min(args.cpu_budget, 8.0))
         if entry["traffic"]:
             entry["traffic_ratio"] = round(entry["traffic"] / r2.bytes, 3)
+        pub = published_of(w2, r2, rf["kernel_us"])
+        if pub:
+            entry["reference_published"] = pub
         chk = oracle_check(w2, r2)
         entry.update({"oracle_check": chk, **t2})
         also.append(entry)
@@ -621,6 +646,9 @@ def driver_mode(args) -> int:
                 "of resident copies for dense workloads)",
         "config": config_of(wl, runner), "roofline": roof, "cpu_baseline": cpu, "also": also,
     }
+    pub = published_of(wl, runner, roof.get("kernel_us"))
+    if pub:
+        line["reference_published"] = pub
     print(json.dumps(line), flush=True)
     return 0 if correct else 1
 

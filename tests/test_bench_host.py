@@ -57,3 +57,24 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "--gpus 2 is not supported" in r.stderr
+
+
+def test_published_figures_name_existing_workloads_and_convert_to_their_unit():
+    from ferret_amd import workloads as W
+
+    class R:  # the Runner fields published_of reads
+        pass
+
+    for key, p in bench.PUBLISHED.items():
+        wl = W.WORKLOADS[key]
+        assert p["unit"] == "TFLOP/s" and p["value"] > 0 and p["source"]
+        r = R()
+        r.flops = W.flops(wl)
+        # a kernel time at which this run matches the published figure exactly
+        us = r.flops / (p["value"] * 1e12) * 1e6
+        got = bench.published_of(wl, r, us)
+        assert got["ratio"] == pytest.approx(1.0, abs=1e-3) and got["this_run"] == pytest.approx(p["value"], rel=1e-3)
+        assert bench.published_of(wl, r, 0.0) is None
+    # GateUp M=16: 2 * 16 * 24576 * 4096 flops; the reference's kernel runs them at 62.91 TFLOP/s
+    assert W.flops(W.WORKLOADS["qwen3_gateup_M16"]) == 2 * 16 * 24576 * 4096
+    assert bench.published_of(W.WORKLOADS["dsv3_fp8_M4096"], R(), 100.0) is None
