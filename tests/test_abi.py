@@ -71,6 +71,31 @@ def test_argument_errors_are_returned_not_raised_without_gpu():
     assert L.ferret_moe_combine(1, 1, 4, 0, 128, 1, None) == -2
 
 
+def test_fp8_entries_reject_before_launch_without_gpu():
+    """The dense and grouped FP8 entry points (and their flag variants) return
+    their codes before any HIP call; the pointers are never dereferenced."""
+    from ferret_amd import lib
+    if not os.path.exists(lib.LIB_PATH):
+        pytest.skip("libferret_hip.so not built")
+    L = lib.load()
+    # dense: a NULL operand, N not a multiple of 128 above 16 rows, K/128 > 128, unknown flag bits
+    assert L.ferret_fp8_gemm_blockscale(1, None, 1, 1, 1, 64, 4096, 7168, None, 0, None) == -1
+    assert L.ferret_fp8_gemm_blockscale(1, 1, 1, 1, 1, 64, 144, 7168, None, 0, None) == -2
+    assert L.ferret_fp8_gemm_blockscale(1, 1, 1, 1, 1, 64, 4096, 128 * 129, None, 0, None) == -2
+    assert L.ferret_fp8_gemm_blockscale_ex(1, 1, 1, 1, 1, 64, 4096, 7168, None, 0, 2, None) == -2
+    # grouped w13: NULL tile table, N % 256, tile_m other than 16 / 128, unknown flag bits
+    args = [1, 1, 1, 1, 1, 1, 1, 320, 16, 128, 8, 256, 4096, 7168, 1]
+    bad = list(args); bad[5] = None
+    assert L.ferret_moe_w13_fp8(*bad, None) == -1
+    bad = list(args); bad[12] = 4096 + 128
+    assert L.ferret_moe_w13_fp8(*bad, None) == -2
+    bad = list(args); bad[8] = 32
+    assert L.ferret_moe_w13_fp8(*bad, None) == -2
+    assert L.ferret_moe_w13_fp8_ex(*args, 4, None) == -2
+    # grouped w2: unknown flag bits
+    assert L.ferret_moe_w2_fp8_ex(1, 1, 1, 1, 1, 1, 1, 10, 16, 64, 8, 7168, 2048, 1, 8, None) == -2
+
+
 def test_noalloc_linear_rejects_oversized_partials_without_gpu():
     """ferret_linear_bf16_noalloc checks its array limit before any HIP call."""
     from ferret_amd import lib
