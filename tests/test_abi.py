@@ -176,3 +176,20 @@ def test_int4_tiled_python_wrappers_check_before_launch():
         ops.moe_w13_w4a16(x, torch.zeros((2, 4, 3, 16, 16), dtype=torch.int32), ws, r)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.moe_w13_w4a16(x, torch.zeros((2, 4, 2, 16, 16), dtype=torch.int32), ws, r)
+
+
+def test_integration_stubs_match_the_library_signatures():
+    """The ctypes stubs INTEGRATION.md shows a maintainer agree with lib.SIGNATURES."""
+    import ctypes
+    import re
+    from ferret_amd import lib
+    text = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
+    env = {"vp": ctypes.c_void_p, "i32": ctypes.c_int, "sz": ctypes.c_size_t}
+    found = {}
+    for name, expr in re.findall(r"L\.(ferret_\w+)\.argtypes(?:, L\.\w+\.restype)? = (\[[^\n`]*?\](?: \* \d+)?"
+                                 r"(?: \+ \[[^\n`]*?\](?: \* \d+)?)*)", text):
+        found[name] = eval(expr, {}, env)  # noqa: S307 -- the doc's own list expressions
+    assert len(found) == 19  # 15 entry points, 3 sizing helpers, the allocation-free linear
+    for name, argtypes in found.items():
+        assert name in lib.SIGNATURES, name
+        assert argtypes == list(lib.SIGNATURES[name][1]), name
