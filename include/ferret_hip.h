@@ -184,7 +184,11 @@ int ferret_moe_w13_fp8(const void* x, const float* sx, const void* w, const floa
  * apply_moe_activation(SILU) of baselines/kimi-moe-w13-int4/baseline_marlin.py:139-168;
  * numerics of correctness/compare_marlin_vs_ref.py:44-100; layout of
  * tasks/kimi-moe-w13-int4-grouped-gemm.yaml:68-83.
- * Requirements: N % 32 == 0, K % 128 == 0, tile_m == 16.
+ * Requirements: N % 32 == 0, K % 128 == 0, tile_m == 16.  Group scales must be
+ * finite with |s| < 2^128 / 1032 (about 3.3e35): the in-register dequant forms
+ * -1032 * s in fp32.  Within that range every weight equals the reference's
+ * bf16_RNE(float(q) * s) bit for bit (tests/test_gpu_int4_scales.py checks all
+ * 65,536 bf16 scale patterns against all 16 nibbles).
  */
 int ferret_moe_w13_w4a16(const void* x, const int32_t* wq, const void* ws,
                          const int32_t* sorted_pair, const int32_t* tiles, const int32_t* ntiles,
