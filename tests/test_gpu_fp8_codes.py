@@ -1,0 +1,66 @@
+"""Every OCP e4m3 code through every FP8 GEMM kernel, exactly.
+
+With unit block scales, one operand one-hot (the code of 1.0 at one K index
+per row) and the other carrying every non-NaN e4m3 code, each output is a
+single e4m3 value, which bf16 holds exactly: c[m, n] = b[n, m % K] (codes on
+the weight side) or a[m, n % K] (codes on the token side).  The shapes pick
+the square kernel (M = N = 4096), the 256 x 128 tiled kernel (M = 300), its
+split-K form (M = 128) and the decode stream kernel (M = 16, M = 1), so the
+widening of both operands in each kernel is checked code by code against the
+oracle's decoding of the code.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as F
+from tests.gpu_helpers import bf16_out
+
+pytestmark = pytest.mark.gpu
+
+ONE = 0x38  # e4m3 1.0
+
+
+@pytest.fixture(scope="module")
+def ops(hip):
+    from ferret_amd import ops as O
+    return O
+
+
+def _codes(rows, K):
+    """Every code in turn (NaN codes 0x7F / 0xFF replaced by 0)."""
+    c = (np.arange(rows * K, dtype=np.int64) * 7 + np.arange(rows * K, dtype=np.int64) // 256) % 256
+    c = c.astype(np.uint8).reshape(rows, K)
+    c[(c & 0x7F) == 0x7F] = 0
+    return c
+
+
+def _one_hot(rows, K):
+    c = np.zeros((rows, K), dtype=np.uint8)
+    c[np.arange(rows), np.arange(rows) % K] = ONE
+    return c
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 256), (300, 512, 384), (128, 512, 512), (16, 1024, 512),
+                                   (1, 512, 256)])
+@pytest.mark.parametrize("side", ["weights", "tokens"])
+def test_every_e4m3_code_exactly(ops, M, N, K, side):
+    print(f"[case] e4m3 codes M={M} N={N} K={K} codes on {side}", flush=True)
+    if side == "weights":
+        a_np, b_np = _one_hot(M, K), _codes(N, K)
+        want = F.e4m3_to_f32(b_np)[:, np.arange(M) % K].T                     # [M, N]
+    else:
+        a_np, b_np = _codes(M, K), _one_hot(N, K)
+        want = F.e4m3_to_f32(a_np)[:, np.arange(N) % K]                       # [M, N]
+    codes = np.unique(b_np if side == "weights" else a_np)
+    assert len(codes) == 254                                                   # all but the two NaNs
+    a = torch.from_numpy(a_np).cuda().view(torch.float8_e4m3fn)
+    b = torch.from_numpy(b_np).cuda().view(torch.float8_e4m3fn)
+    sa = torch.ones((M, K // 128), dtype=torch.float32, device="cuda")
+    sb = torch.ones((N // 128, K // 128), dtype=torch.float32, device="cuda")
+    out = ops.fp8_gemm_blockscale(a, sa, b, sb)
+    torch.cuda.synchronize()
+    got = bf16_out(out)
+    same = got == want                                                         # +0 == -0
+    bad = np.argwhere(~same)
+    assert same.all(), f"{len(bad)} outputs differ, first (m, n) = {bad[:3].tolist()}"
