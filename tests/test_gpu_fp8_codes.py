@@ -7,7 +7,8 @@ the weight side) or a[m, n % K] (codes on the token side).  The shapes pick
 the square kernel (M = N = 4096), the 256 x 128 tiled kernel (M = 300), its
 split-K form (M = 128) and the decode stream kernel (M = 16, M = 1), so the
 widening of both operands in each kernel is checked code by code against the
-oracle's decoding of the code.
+oracle's decoding of the code.  The grouped down projection (routed rows, one
+expert empty) gets the same check on both tile tables.
 """
 import numpy as np
 import pytest
@@ -64,3 +65,41 @@ def test_every_e4m3_code_exactly(ops, M, N, K, side):
     same = got == want                                                         # +0 == -0
     bad = np.argwhere(~same)
     assert same.all(), f"{len(bad)} outputs differ, first (m, n) = {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("tile_m,rows", [(16, [20, 0, 37, 3]), (128, [140, 0, 300, 17])])
+@pytest.mark.parametrize("side", ["weights", "tokens"])
+def test_every_e4m3_code_through_the_grouped_down_projection(ops, tile_m, rows, side):
+    """The same through moe_w2_fp8 (routed rows, pair order), on the decode
+    (16-row) and prefill (128-row) tile tables: out[p, n] = w[e_p, n, p % K]
+    or h[p, n % K]."""
+    N, K = 512, 384
+    print(f"[case] e4m3 codes w2 tile_m={tile_m} codes on {side}", flush=True)
+    E = len(rows)
+    ids_np = np.concatenate([np.full(n, e, dtype=np.int32) for e, n in enumerate(rows)])
+    np.random.default_rng(tile_m).shuffle(ids_np)
+    P = len(ids_np)
+    if side == "weights":
+        h_np = _one_hot(P, K)
+        w_np = np.stack([_codes(N, K) for _ in range(E)])
+        want = F.e4m3_to_f32(w_np)[ids_np[:, None], np.arange(N)[None, :], (np.arange(P) % K)[:, None]]
+        codes = np.unique(w_np)
+    else:
+        h_np = _codes(P, K)
+        w_np = np.stack([_one_hot(N, K) for _ in range(E)])
+        want = F.e4m3_to_f32(h_np)[:, np.arange(N) % K]
+        codes = np.unique(h_np)
+    assert len(codes) == 254
+    h = torch.from_numpy(h_np).cuda().view(torch.float8_e4m3fn)
+    w = torch.from_numpy(np.ascontiguousarray(w_np)).cuda().view(torch.float8_e4m3fn)
+    sh = torch.ones((P, K // 128), dtype=torch.float32, device="cuda")
+    sw = torch.ones((E, N // 128, K // 128), dtype=torch.float32, device="cuda")
+    ids = torch.from_numpy(ids_np.reshape(-1, 1)).cuda()
+    rt = ops.moe_permute(ids, E, tile_m)
+    out = torch.full((P, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.moe_w2_fp8(h, sh, w, sw, rt, out=out)
+    torch.cuda.synchronize()
+    got = bf16_out(out)
+    same = got == want
+    bad = np.argwhere(~same)
+    assert same.all(), f"{len(bad)} outputs differ, first (p, n) = {bad[:3].tolist()}"
