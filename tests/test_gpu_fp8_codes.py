@@ -103,3 +103,34 @@ def test_every_e4m3_code_through_the_grouped_down_projection(ops, tile_m, rows, 
     same = got == want
     bad = np.argwhere(~same)
     assert same.all(), f"{len(bad)} outputs differ, first (p, n) = {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("tile_m,rows", [(16, [20, 0, 37, 3]), (128, [140, 0, 300, 17])])
+def test_every_e4m3_code_through_the_grouped_gate_up_projection(ops, tile_m, rows):
+    """moe_w13_fp8 with every gate weight 32.0 and one-hot activations: gate =
+    32 and silu(32) = 32 in fp32 (exp(-32) < 2^-24), so out[p, n] = 32 *
+    up[e_p, n, t % K] exactly, with every code on the up rows."""
+    N, K = 512, 384
+    print(f"[case] e4m3 codes w13 tile_m={tile_m}", flush=True)
+    E = len(rows)
+    ids_np = np.concatenate([np.full(n, e, dtype=np.int32) for e, n in enumerate(rows)])
+    np.random.default_rng(tile_m + 1).shuffle(ids_np)
+    T = len(ids_np)
+    x_np = _one_hot(T, K)
+    up = np.stack([_codes(N // 2, K) for _ in range(E)])
+    w_np = np.concatenate([np.full((E, N // 2, K), 0x60, dtype=np.uint8), up], axis=1)  # 0x60 = 32.0
+    assert F.e4m3_to_f32(np.array([0x60], dtype=np.uint8))[0] == 32.0 and len(np.unique(up)) == 254
+    want = 32.0 * F.e4m3_to_f32(up)[ids_np[:, None], np.arange(N // 2)[None, :], (np.arange(T) % K)[:, None]]
+    x = torch.from_numpy(x_np).cuda().view(torch.float8_e4m3fn)
+    w = torch.from_numpy(np.ascontiguousarray(w_np)).cuda().view(torch.float8_e4m3fn)
+    sx = torch.ones((T, K // 128), dtype=torch.float32, device="cuda")
+    sw = torch.ones((E, N // 128, K // 128), dtype=torch.float32, device="cuda")
+    ids = torch.from_numpy(ids_np.reshape(-1, 1)).cuda()
+    rt = ops.moe_permute(ids, E, tile_m)
+    out = torch.full((T, N // 2), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.moe_w13_fp8(x, sx, w, sw, rt, out=out)
+    torch.cuda.synchronize()
+    got = bf16_out(out)
+    same = got == want
+    bad = np.argwhere(~same)
+    assert same.all(), f"{len(bad)} outputs differ, first (t, n) = {bad[:3].tolist()}"
