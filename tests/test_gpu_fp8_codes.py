@@ -134,3 +134,44 @@ def test_every_e4m3_code_through_the_grouped_gate_up_projection(ops, tile_m, row
     same = got == want
     bad = np.argwhere(~same)
     assert same.all(), f"{len(bad)} outputs differ, first (t, n) = {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 2048), (300, 2048, 2048)])
+@pytest.mark.parametrize("side", ["weights", "tokens"])
+def test_every_ue8m0_scale_byte_exactly(ops, M, N, K, side):
+    """UE8M0 mode: unit e4m3 values, one side one-hot, and every scale byte
+    1..254 on the other side's blocks (byte 127 on this side), so c[m, n] =
+    2^(e - 127) exactly for the byte e of its block.  M = N = 4096 runs the
+    square kernel with the bytes folded into the widening; M = 300 the decoded
+    fp32 scales through the tiled kernel."""
+    print(f"[case] ue8m0 bytes M={M} N={N} K={K} bytes on {side}", flush=True)
+    nk = K // 128
+    if side == "weights":
+        a_np = _one_hot(M, K)
+        b_np = np.full((N, K), ONE, dtype=np.uint8)
+        blk = (np.arange(N // 128)[:, None] * nk + np.arange(nk)[None, :])
+        eb = (1 + blk % 254).astype(np.uint8)                                   # [N/128, nk]
+        ue_a = np.full((M, nk), 127, dtype=np.uint8)
+        ue_b = np.repeat(eb, 128, axis=0)                                       # one row per weight row
+        want = np.ldexp(1.0, eb[(np.arange(N) // 128)[None, :], ((np.arange(M) % K) // 128)[:, None]].astype(np.int64)
+                        - 127).astype(np.float32)
+        used = np.unique(eb)
+    else:
+        a_np = np.full((M, K), ONE, dtype=np.uint8)
+        b_np = _one_hot(N, K)
+        ea = (1 + (np.arange(M)[:, None] * nk + np.arange(nk)[None, :]) % 254).astype(np.uint8)   # [M, nk]
+        ue_a = ea
+        ue_b = np.full((N, nk), 127, dtype=np.uint8)
+        want = np.ldexp(1.0, ea[:, ((np.arange(N) % K) // 128)].astype(np.int64) - 127).astype(np.float32)
+        used = np.unique(ea)
+    assert len(used) == 254 and used.min() == 1 and used.max() == 254
+    a = torch.from_numpy(a_np).cuda().view(torch.float8_e4m3fn)
+    b = torch.from_numpy(b_np).cuda().view(torch.float8_e4m3fn)
+    sfa = ops.pack_ue8m0(torch.from_numpy(ue_a).cuda())
+    sfb = ops.pack_ue8m0(torch.from_numpy(np.ascontiguousarray(ue_b)).cuda())
+    out = ops.fp8_gemm_ue8m0(a, sfa, b, sfb)
+    torch.cuda.synchronize()
+    got = bf16_out(out)
+    same = got == want
+    bad = np.argwhere(~same)
+    assert same.all(), f"{len(bad)} outputs differ, first (m, n) = {bad[:3].tolist()}"
