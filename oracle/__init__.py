@@ -1,8 +1,8 @@
 """CPU oracle for the quantized-GEMM path — TEST INFRASTRUCTURE ONLY.
 
 This package restates, in numpy on the CPU, the algorithm of every function on
-the hot path so that the HIP kernels can be checked against it.  It is the
-checker, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
+the hot path so that the HIP kernels can be checked against it.  It is what
+the tests compare with, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it.  The ``ferret_amd`` package
 never imports it and has no CPU fallback.
 

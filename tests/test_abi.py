@@ -179,7 +179,8 @@ def test_int4_tiled_python_wrappers_check_before_launch():
 
 
 def test_integration_stubs_match_the_library_signatures():
-    """The ctypes stubs INTEGRATION.md shows a maintainer agree with lib.SIGNATURES."""
+    """The ctypes stubs the integration guide at the repository root shows a
+    maintainer agree with lib.SIGNATURES."""
     import ctypes
     import re
     from ferret_amd import lib

@@ -1,16 +1,16 @@
 """CPU proof that the stream kernel's launch plan stays in bounds.
 
 Compiles ferret_amd/csrc/stream_plan.hpp (the host-only plan that try_stream in
-skinny.hip uses) with g++ together with a small checker, and walks every
+skinny.hip uses) with g++ together with a small bounds walker, and walks every
 work-group of every configuration the library instantiates, over a sweep of
 shapes, tile counts, split counts and grid sizes.  For each plan the shape is
-accepted for, the checker follows the kernel's index arithmetic
+accepted for, the walk follows the kernel's index arithmetic
 (stream_kernel.hpp: unit -> split, token tile, row unit; rows of a unit's
 blocks; each wave's K-steps; the span of the tile table a work-group copies to
 LDS) and fails if any unit addresses a weight row >= N, an output row past the
 output, a K-step >= K / 128, or a tile-table span > kStreamMaxTiles.  The
 configuration that once faulted the GPU (two 16-row blocks per unit while the
-unit count assumed one) is a mutant of the plan that the checker rejects.
+unit count assumed one) is a mutant of the plan that the walk rejects.
 """
 import os
 import shutil
@@ -125,7 +125,7 @@ def test_every_instantiated_stream_plan_stays_in_bounds(tmp_path):
     assert plans > 1000, res.stdout            # the sweep reaches many accepted shapes
 
 
-def test_checker_rejects_the_rb_mismatch_that_faulted(tmp_path):
+def test_walker_rejects_the_rb_mismatch_that_faulted(tmp_path):
     exe = _build(tmp_path, "MUTANT_RB_MISMATCH")
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert res.returncode != 0 and "weight row >= N" in res.stdout
@@ -143,20 +143,20 @@ def _instantiations():
     return calls, src.count("try_stream<")   # the template's definition is `try_stream(`
 
 
-def _checker_cfgs():
+def _walker_cfgs():
     import re
     body = CHECKER[CHECKER.index("kCfgs[] = {"):CHECKER.index("};", CHECKER.index("kCfgs[] = {"))]
     return {(m.group(1) == "true", int(m.group(2)), int(m.group(3)), m.group(4) == "true")
             for m in re.finditer(r'\{"[^"]*",\s*(true|false),\s*(\d+),\s*(\d+),\s*(true|false),\s*\d+\}', body)}
 
 
-def test_checker_covers_every_try_stream_instantiation():
+def test_walker_covers_every_try_stream_instantiation():
     """kCfgs above is written by hand: every try_stream instantiation in
     skinny.hip must appear in it, so an added or changed one cannot escape the
     bounds walk."""
     calls, n_sites = _instantiations()
     assert len(calls) == n_sites >= 9, (len(calls), n_sites)   # the regex saw every call site
-    cfgs = _checker_cfgs()
+    cfgs = _walker_cfgs()
     assert len(cfgs) >= 6   # distinct (silu, RB, NW, grouped) tuples of the eight entries
     missing = sorted(set(calls) - cfgs)
-    assert not missing, f"try_stream instantiations not walked by the checker (silu, RB, NW, grouped): {missing}"
+    assert not missing, f"try_stream instantiations not walked by the plan walk (silu, RB, NW, grouped): {missing}"
