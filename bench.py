@@ -768,7 +768,7 @@ def main(argv=None) -> int:
     global INT4_LAYOUT
     INT4_LAYOUT = args.int4_layout
     if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the quantized-GEMM path on "
+        print(f"bench.py: --gpus {args.gpus} is not supported: this benchmark measures the quantized-GEMM path on "
               "one GPU only (no collective or sharded step exists). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.also is None:

@@ -2,7 +2,7 @@
 // (bf16 -> OCP e4m3 + fp32 scales, the input format of every FP8 GEMM here)
 // and the top-k weighted combine of the w2 (down) outputs.
 //
-// Quantizer (the build's absmax/448 rule; the reference calls DeepGEMM's
+// Quantizer (the library's absmax/448 rule; the reference calls DeepGEMM's
 // per_token_cast_to_fp8 at baselines/fp8-gemm/baseline_prefill.py:41, whose
 // epsilon clamp is not vendored):
 //   amax = max(max_{k in block} |x[m,k]|, 1e-4)

@@ -1,6 +1,6 @@
 """task.yaml loading and KERNEL_RESULT scoring, behaviour-compatible with ferret.
 
-Mirrors the reference's scoring surface so that bench output from this build is
+Mirrors the reference's scoring surface so that bench output from this library is
 parsed and scored unchanged:
 
 * ``load_task_spec``      — loads the task.yaml schema of tasks/template.yaml (this

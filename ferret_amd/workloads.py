@@ -6,7 +6,7 @@ projections from M = 1 to 8192), plus the rest of the FP8 MoE layer: the w2
 down projection (K = 2048 -> N = 7168, tasks/fp8-group-gemm-dsv3-decode.yaml:11-13),
 the 1x128 activation quantizer in front of it and the top-k combine after it.
 Inputs are generated with torch on any device from per-tensor seeds;
-the quantizer below is the build's absmax/448 rule (1x128 activation blocks,
+the quantizer below is the library's absmax/448 rule (1x128 activation blocks,
 128x128 weight blocks, fp32 scales), the same rule DeepGEMM's
 per_token_cast_to_fp8 / per_block_cast_to_fp8 implement at the reference's call
 sites (baselines/fp8-gemm/baseline_prefill.py:41-42,

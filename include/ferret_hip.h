@@ -126,7 +126,7 @@ int ferret_fp8_gemm_ue8m0(const void* a, const uint32_t* sfa, const void* b, con
  * (logit desc, expert asc), NaN ranks as -inf; weights[T,topk] (optional,
  * may be NULL) = softmax over all E at the chosen experts.  The reference has
  * no routing kernel (its stand-ins: baselines/kimi-moe-w13-int4/baseline_marlin.py:92-104,
- * baselines/fp8-group-gemm/baseline_dsv3_decode.py:50); this is the build's own
+ * baselines/fp8-group-gemm/baseline_dsv3_decode.py:50); this is the library's own
  * contract.  Requirements: 1 <= topk <= min(E, 16), E <= 1024.
  */
 int ferret_moe_route_topk(const float* logits, int T, int E, int topk, int32_t* ids,
@@ -257,7 +257,7 @@ int ferret_moe_w2_fp8(const void* h, const float* sh, const void* w, const float
  * weights), y bf16 [T, N]; the fp32 sum runs in j order (deterministic).
  * The reference has no combine kernel (its routing weights are computed and
  * left unused by w13: baselines/kimi-moe-w13-int4/baseline_marlin.py:92-104,158);
- * this is the build's own contract.  Requirements: N % 8 == 0, 1 <= topk <= 64.
+ * this is the library's own contract.  Requirements: N % 8 == 0, 1 <= topk <= 64.
  */
 int ferret_moe_combine(const void* o, const float* w, int T, int topk, int N, void* y, void* stream);
 

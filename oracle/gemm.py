@@ -19,7 +19,7 @@ float32, in the reference's summation form:
 * FP8 MoE w2 (down, K = 2048 -> N = 7168 at
   ``tasks/fp8-group-gemm-dsv3-decode.yaml:11-13``): the block-scaled product of
   ``cpu_ref_bs`` per routed pair, the pair's own activation row.
-* Top-k combine: sum_j w[t,j] * o[t*topk+j] in float32 (the build's own
+* Top-k combine: sum_j w[t,j] * o[t*topk+j] in float32 (the library's own
   contract; the reference's routing weights are left unused by w13,
   ``baselines/kimi-moe-w13-int4/baseline_marlin.py:158``).
 

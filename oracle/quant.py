@@ -5,7 +5,7 @@ blocks) and ``per_block_cast_to_fp8`` (128x128 weight blocks) with fp32 scales
 (``baselines/fp8-gemm/baseline_prefill.py:41-42``,
 ``baselines/fp8-group-gemm/baseline_dsv3_decode.py:45-53``).  DeepGEMM is not
 vendored (empty submodule), so its exact epsilon clamp cannot be imported; this
-module defines the build's own quantizer, stated once here and mirrored by the
+module defines the library's own quantizer, stated once here and mirrored by the
 torch input generator:
 
     amax = max(|x| over the block, 1e-4);  q = e4m3_RNE(x * (448 / amax));

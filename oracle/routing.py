@@ -5,7 +5,7 @@ The reference has no routing kernel: DSv3 tasks use synthetic uniform segments
 (``baselines/fp8-group-gemm/baseline_dsv3_decode.py:50``,
 ``baseline_dsv3_prefill.py:53``), and Kimi uses randperm routing plus vLLM's
 ``moe_align_block_size`` (``baselines/kimi-moe-w13-int4/baseline_marlin.py:92-104,123-126``).
-The contract restated here is therefore the build's own, fixed as follows:
+The contract restated here is therefore the library's own, fixed as follows:
 
 * top-k is taken on fp32 LOGITS (softmax is monotonic), ordered by
   (value descending, expert index ascending); NaN logits rank as -inf;
