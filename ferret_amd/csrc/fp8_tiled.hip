@@ -17,7 +17,9 @@
 // tile 256 weight rows x 128 tokens, wave tile 64 x 64 (4 x 4 MFMA tiles).
 // Small M (<= 256) with a workspace: 128 x 128 tiles of 8 waves (64 weight
 // rows x 32 tokens each, again two per SIMD) over K ranges (split-K), fp32
-// partials summed in split order by a reduce kernel.
+// partials summed in split order by a reduce kernel.  Mid M, where 256 x 128
+// tiles would occupy at most half of the CUs: the same 128 x 128 tiles over
+// all of K, storing bf16.
 // Operands go global -> LDS directly (global_load_lds_dwordx4, no VGPR
 // staging) through a 3-stage ring; every load instruction reads complete
 // 128-byte lines; LDS rows of 128 B have their 16-byte chunk index
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 template <bool SILU, bool GROUPED, int WN, bool SPLIT, bool FULL, bool F8 = false, int TW = 2>
 __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
   static_assert(!SILU || GROUPED, "the SiLU epilogue is the grouped w13 GEMM's");
-  static_assert(TW == 2 || SPLIT, "the bf16 and SiLU epilogues take 64-token waves");
+  static_assert(TW == 2 || !SILU, "the SiLU epilogue takes 64-token waves");
   using C = TileCfg<WN, TW>;
   constexpr int MIX = C::kMI, TOKW = C::kTokW;
   constexpr int TB_WN = C::kWN, TB_WAVES = C::kWaves, TB_N = C::kN;
@@ -469,16 +471,17 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
   // ---- epilogue. acc[ni][mi][i]: weight row wfrag_row[ni] - r + 4g + i, token column r.
   if constexpr (!SILU && !SPLIT) {
     // bf16 store.  Every wave has passed the last barrier (all X phases and
-    // stage copies are done), so the ring is idle: the wave stages its 64 x 64
+    // stage copies are done), so the ring is idle: the wave stages its TOKW x 64
     // sub-tile through its own LDS rows (pitch 144 B: the 16 rows of one
     // write land on distinct banks) and stores whole 128-B row segments, 16 B
     // per lane.  Direct 8-B stores (16 rows x 32 B per instruction) took
     // ~2 us per work-group; staged, the short-K GEMMs run 10-15 % faster.
     if (nb * TB_N + wn * 64 >= N) return;  // wave's rows lie past N (N % 256 == 128)
     constexpr int PITCH = 144;
-    uint8_t* stg = lds + wave * 64 * PITCH;
+    static_assert(TB_WAVES * TOKW * PITCH <= C::kLds, "staging fits the ring");
+    uint8_t* stg = lds + wave * TOKW * PITCH;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MIX; ++mi)
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) {
         u32x2 v;
@@ -489,9 +492,9 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own rows are written
     const int chunk = lane & 7;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
+    for (int it = 0; it < TOKW / 8; ++it) {
       const int rw = it * 8 + (lane >> 3);
-      const int tl = wm * 64 + rw;  // token row inside the tile
+      const int tl = wm * TOKW + rw;  // token row inside the tile
       const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rw * PITCH + chunk * 16);
       if (tl < nrows) {
         // dense: token row; grouped: the routed pair of the sorted row
@@ -617,6 +620,17 @@ int ferret_fp8_gemm_tiled(const void* a, const float* sa, const void* b, const f
                  : used == 8 ? splitk_reduce_kernel<8> : splitk_reduce_kernel<0>;
     hipLaunchKernelGGL(reduce, dim3(512), dim3(256), 0, st, p.partial, used, n4, static_cast<uint16_t*>(c));
     return (int)hipGetLastError();
+  }
+  // Mid M: where the 256 x 128 grid would fill at most half of the CUs
+  // (DSv3 q_b_proj at M = 512: 48 work-groups, each over all of K), the
+  // 128 x 128 tiles of the split-K configuration double it while it still
+  // fits one round, and store bf16 directly.
+  const int t256 = ((N + 255) / 256) * p.m_blocks;
+  const int t128 = (N / (64 * SPLITK_WN)) * p.m_blocks;
+  if (2 * t256 <= SPLITK_TARGET && t128 <= SPLITK_TARGET) {
+    p.n_blocks = N / (64 * SPLITK_WN);
+    if (M % TB_M == 0) return launch_tiled<false, false, SPLITK_WN, false, true, SPLITK_TW>(p, dim3(t128), st, f8);
+    return launch_tiled<false, false, SPLITK_WN, false, false, SPLITK_TW>(p, dim3(t128), st, f8);
   }
   // Dense tiles: with every token tile full (M % 128 == 0) the kernel skips
   // the per-wave count of occupied 16-token sub-tiles.
