@@ -233,12 +233,27 @@ def test_fp8_gemm_workspace_and_plain_paths(hip, ops, M, N, K):
         assert_gemm_close(bf16_out(c), ref, f"fp8 {tag} M={M}")
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 256, 128), (256, 256, 256), (384, 512, 384), (512, 256, 640)])
-def test_fp8_gemm_staggered_short_k(hip, M, N, K):
-    """Full 128-row token tiles without a workspace take the staggered
+def _tile_config(M, N):
+    """The tiled configuration of a shape run without a workspace, by the dispatch
+    rule of ferret_fp8_gemm_tiled: 128 x 128 tiles where the 256 x 128 grid
+    would fill at most half of 256 CUs and the 128 x 128 grid fits them."""
+    mb = -(-M // 128)
+    t256, t128 = -(-N // 256) * mb, (N // 128) * mb
+    return "128x128" if 2 * t256 <= 256 and t128 <= 256 else "256x128"
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (128, 256, 128, "128x128"), (256, 256, 256, "128x128"), (384, 512, 384, "128x128"), (512, 256, 640, "128x128"),
+    (520, 3072, 1536, "128x128"), (1000, 1024, 512, "128x128"),
+    (1152, 4096, 128, "256x128"), (1152, 4096, 256, "256x128"), (1100, 4096, 384, "256x128"),
+    (1100, 4096, 640, "256x128")])
+def test_fp8_gemm_staggered_short_k(hip, M, N, K, cfg):
+    """Without a workspace both tiled configurations run the staggered
     two-half loop; K of 1, 2, 3 and 5 K-steps covers its prologue (three
-    stages in flight for one half) and its last-stage waits."""
-    _say(f"fp8_gemm staggered M={M} N={N} K={K}")
+    stages in flight for one half) and its last-stage waits, on full and
+    partial last token tiles (M % 128 != 0), above M = 256 too."""
+    assert _tile_config(M, N) == cfg
+    _say(f"fp8_gemm staggered M={M} N={N} K={K} ({cfg} tiles)")
     a, sa, b, sb = _fp8_inputs(M, N, K, seed=11 * M + K)
     ref = G.fp8_blockscale_gemm(codes8(a), f32(sa), codes8(b), f32(sb))
     c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
