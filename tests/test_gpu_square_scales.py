@@ -40,9 +40,11 @@ def _wide_scales(rng, M, N, K):
 
 
 # (3072, 4096) and (3000, 4096): 192 square-kernel tiles (the second with a
-# partial last token tile); (1000, 4096): 128 tiles, below the square kernel's
-# threshold, so the 256 x 128 tiled kernel (per-block folds) runs the same check.
-@pytest.mark.parametrize("M,N,K", [(3072, 4096, 1024), (3000, 4096, 1024), (1000, 4096, 1024)])
+# partial last token tile).  Below the square kernel's threshold the tiled
+# kernel (per-block folds) runs the same check: (1100, 4096) on 144 tiles of
+# 256 x 128, and (1000, 4096), whose 128 such tiles would fill half the CUs,
+# on 256 tiles of 128 x 128 (both with a partial last token tile).
+@pytest.mark.parametrize("M,N,K", [(3072, 4096, 1024), (3000, 4096, 1024), (1100, 4096, 1024), (1000, 4096, 1024)])
 def test_square_kernel_scales_over_80_octaves(hip, M, N, K):
     from ferret_amd import ops
     L = hip
