@@ -68,7 +68,7 @@ FAMILIES = {
                                  "dsv3_o_proj_M4096", "dsv3_o_proj_M8192"],
     "moe_ep8_decode": [f"dsv3_ep8_{p}_M{m}" for m in (1, 4, 8, 16) for p in ("gate_up", "down")],
     "moe_ep8_prefill": [f"dsv3_ep8_{p}_M{m}" for m in (64, 128, 256, 512) for p in ("gate_up", "down")],
-    "kimi_tp8": ["kimi_w4a16_w13_T8_tp8"],
+    "kimi_tp8": ["kimi_w4a16_w13_T1_tp8", "kimi_w4a16_w13_T8_tp8"],
 }
 DENSE_KINDS = ("linear_bf16", "fp8_gemm", "fp8_gemm_ue8m0", "quant_act", "moe_combine")
 # `also` workloads measured like the default one (in-run traffic, own CPU
@@ -87,6 +87,11 @@ PUBLISHED = {
                                       "(vLLM Marlin on the same B200: 9.36)",
                               "source": "correctness/kimi-moe-w13-precision-fix.md:14, "
                                         "tasks/kimi-moe-w13-int4-grouped-gemm.yaml:102"},
+    "kimi_w4a16_w13_T1_tp8": {"value": 2.96, "unit": "TFLOP/s", "hardware": "B200",
+                              "what": "the reference's best INT4 w13 kernel, 128 MB flush before each launch "
+                                      "(vLLM Marlin on the same B200: 2.29)",
+                              "source": "correctness/kimi-moe-w13-precision-fix.md:13, "
+                                        "tasks/kimi-moe-w13-int4-grouped-gemm.yaml:101"},
 }
 MOE_KINDS = ("moe_fp8", "moe_w4a16", "moe_fp8_w2")
 FAMILIES["all"] = list(dict.fromkeys(

@@ -94,10 +94,14 @@ WORKLOADS: dict[str, Workload] = {w.key: w for w in [
       for m in (1, 4, 8, 16, 64, 128, 256, 512)
       for i, (proj, kind, k, n) in enumerate([("gate_up", "moe_fp8", 7168, 4096),
                                              ("down", "moe_fp8_w2", 2048, 7168)])],
-    # tasks/kimi-moe-w13-int4-grouped-gemm.yaml:35-40 (TP 8 rank: N_r = 2 I_r = 512)
+    # tasks/kimi-moe-w13-int4-grouped-gemm.yaml:35-40 (TP 8 rank: N_r = 2 I_r = 512); the reference
+    # measures T = 1 and T = 8 (correctness/kimi-moe-w13-precision-fix.md:13-14)
     Workload("kimi_w4a16_w13_T8_tp8", "moe_w4a16", N=512, K=7168, T=8, E=384, topk=8, routing="softmax",
              description="Kimi-K2 INT4 W4A16 MoE w13, TP8 rank: 8 tokens, top-8 of 384, N_r=512",
              seeds={"logits": 18, "x": 19, "w": 900}),
+    Workload("kimi_w4a16_w13_T1_tp8", "moe_w4a16", N=512, K=7168, T=1, E=384, topk=8, routing="softmax",
+             description="Kimi-K2 INT4 W4A16 MoE w13, TP8 rank: 1 token, top-8 of 384, N_r=512",
+             seeds={"logits": 16, "x": 17, "w": 901}),
     Workload("dsv3_moe_w13_decode", "moe_fp8", N=4096, K=7168, T=128, E=256, topk=8, routing="softmax",
              description="DSv3 FP8 MoE w13 decode: 128 tokens, top-8 of 256", seeds={"logits": 5, "x": 6, "w": 100}),
     Workload("kimi_w4a16_w13_decode", "moe_w4a16", N=4096, K=7168, T=64, E=384, topk=8, routing="softmax",

@@ -57,7 +57,7 @@ def test_int4_tile_weights_full_size_sampled_experts(ops):
         assert np.array_equal(t[e:e + 1].cpu().numpy(), FM.int4_tile_weights(inp["w"][e:e + 1].cpu().numpy()))
 
 
-@pytest.mark.parametrize("key", ["kimi_w4a16_w13_decode", "kimi_w4a16_w13_T8_tp8"])
+@pytest.mark.parametrize("key", ["kimi_w4a16_w13_decode", "kimi_w4a16_w13_T8_tp8", "kimi_w4a16_w13_T1_tp8"])
 def test_tiled_decode_bit_identical_full_size(ops, key):
     """The bench workloads: the tiled path equals the checkpoint-layout path
     (itself checked against the oracle at this size in test_gpu_parity)."""

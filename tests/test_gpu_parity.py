@@ -464,7 +464,8 @@ def test_dense_full_size(ops, key):
 
 
 @pytest.mark.parametrize("key", ["dsv3_moe_w13_decode", "kimi_w4a16_w13_decode", "dsv3_moe_w13_prefill",
-                                 "kimi_w4a16_w13_T8_tp8", "dsv3_moe_w2_decode", "dsv3_moe_w2_prefill"]
+                                 "kimi_w4a16_w13_T8_tp8", "kimi_w4a16_w13_T1_tp8", "dsv3_moe_w2_decode",
+                                 "dsv3_moe_w2_prefill"]
                          + [f"dsv3_ep8_{p}_M{m}" for m in (1, 16, 64, 512) for p in ("gate_up", "down")])
 def test_moe_full_size(ops, key):
     from ferret_amd import workloads as W
