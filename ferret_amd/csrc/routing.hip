@@ -25,16 +25,53 @@ __device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
   return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
-// One wave per token; each lane owns experts lane, lane+64, ...
+// Order key of a (logit, expert) pair as two words compared lexicographically:
+// hi = the logit's bits mapped to unsigned order (NaN taken as -inf, -0 as +0,
+// which ties +0), lo = ~expert; a larger key is a larger logit, then a smaller
+// expert -- the (logit desc, expert asc) order.  Slots past E get (0, 0), below
+// every real pair (the smallest real hi, that of -inf, is 0x007FFFFF).
+__device__ __forceinline__ uint32_t order_bits(float x) {
+  if (x != x) x = -INFINITY;
+  if (x == 0.f) x = 0.f;
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_order_bits(uint32_t h) {
+  return __uint_as_float((h & 0x80000000u) ? (h & 0x7FFFFFFFu) : ~h);
+}
+__device__ __forceinline__ bool key_gt(uint32_t h1, uint32_t l1, uint32_t h2, uint32_t l2) {
+  return h1 > h2 || (h1 == h2 && l1 > l2);
+}
+// One step of a wave max over keys: each lane of the rows in ROWS takes the
+// larger of its key and that of the lane the DPP control names; lanes of the
+// other rows read their own key (the `old` operand) and keep it.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ void key_max_dpp(uint32_t& h, uint32_t& l) {
+  const uint32_t ph = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROWS, 0xF, false);
+  const uint32_t pl = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROWS, 0xF, false);
+  if (key_gt(ph, pl, h, l)) {
+    h = ph;
+    l = pl;
+  }
+}
+
+// One wave per token; lane l owns experts l, l + 64, ... (PER slots, E <= 64 PER).
+// Each of the topk rounds takes the wave's largest untaken key: every lane
+// offers its best untaken slot, four DPP steps (quad xor 1, quad xor 2, half-row
+// mirror, row mirror) leave each 16-lane row's maximum in all of its lanes, two
+// row broadcasts carry the maximum to lane 63, and its key, read into scalar
+// registers, names the winner.  The owning lane marks the slot taken.  Weights: the full softmax over E at the
+// chosen experts (not renormalised).
+template <int PER>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T, int E,
                                                           int topk, int32_t* __restrict__ ids,
                                                           float* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
+  if (t >= T) return;  // wave-uniform: the rest of the wave runs with all 64 lanes
   const float* row = logits + (size_t)t * E;
-  constexpr int PER = kMaxE / 64;
   float v[PER];
+  uint32_t kh[PER], kl[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int ex = lane + 64 * i;
@@ -44,70 +81,93 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
       if (x != x) x = -INFINITY;
     }
     v[i] = x;
+    kh[i] = ex < E ? order_bits(x) : 0u;
+    kl[i] = ex < E ? ~(uint32_t)ex : 0u;
   }
-  uint32_t taken = 0;  // bit i: v[i] already selected
-  float sel_v[kMaxTopk] = {};
-  int sel_i[kMaxTopk] = {};
+  uint32_t taken = 0;  // bit i: slot i already selected
+  int my_id = 0;       // lane k < topk: the k-th expert
+  float my_v = 0.f;
+  uint32_t top_h = 0;  // key of the first pick (the row maximum)
+  for (int k = 0; k < topk; ++k) {
+    uint32_t bh = 0, bl = 0;
 #pragma unroll
-  for (int k = 0; k < kMaxTopk; ++k) {
-    if (k >= topk) break;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int ex = lane + 64 * i;
-      if (ex < E && !((taken >> i) & 1u) && better(v[i], ex, bv, bi)) {
-        bv = v[i];
-        bi = ex;
+    for (int i = 0; i < PER; ++i)
+      if (!((taken >> i) & 1u) && key_gt(kh[i], kl[i], bh, bl)) {
+        bh = kh[i];
+        bl = kl[i];
       }
+    key_max_dpp<0xB1>(bh, bl);        // quad_perm [1, 0, 3, 2]
+    key_max_dpp<0x4E>(bh, bl);        // quad_perm [2, 3, 0, 1]
+    key_max_dpp<0x141>(bh, bl);       // row_half_mirror
+    key_max_dpp<0x140>(bh, bl);       // row_mirror: each row's maximum in all its lanes
+    key_max_dpp<0x142, 0xA>(bh, bl);  // row_bcast:15 into rows 1 and 3
+    key_max_dpp<0x143, 0xC>(bh, bl);  // row_bcast:31 into rows 2 and 3: lane 63 holds the maximum
+    const uint32_t wh = (uint32_t)__builtin_amdgcn_readlane((int)bh, 63);
+    const uint32_t wl = (uint32_t)__builtin_amdgcn_readlane((int)bl, 63);
+    const int sel = (int)~wl;
+    if ((sel & 63) == lane) taken |= 1u << (sel >> 6);
+    if (k == lane) {
+      my_id = sel;
+      my_v = from_order_bits(wh);
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    sel_v[k] = bv;
-    sel_i[k] = bi;
+    if (k == 0) top_h = wh;
   }
-  if (lane < topk) {
-    int myi = 0;
-#pragma unroll
-    for (int k = 0; k < kMaxTopk; ++k)
-      if (k < topk && k == lane) myi = sel_i[k];
-    ids[(size_t)t * topk + lane] = myi;
-  }
+  if (lane < topk) ids[(size_t)t * topk + lane] = my_id;
   if (weights) {
-    const float mx = sel_v[0];
+    const float mx = from_order_bits(top_h);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       if (lane + 64 * i < E) s += expf(v[i] - mx);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if (lane < topk) {
-      float mv = 0.f;
-#pragma unroll
-      for (int k = 0; k < kMaxTopk; ++k)
-        if (k < topk && k == lane) mv = sel_v[k];
-      weights[(size_t)t * topk + lane] = expf(mv - mx) / s;
-    }
+    if (lane < topk) weights[(size_t)t * topk + lane] = expf(my_v - mx) / s;
   }
 }
 
-// Inclusive Hillis-Steele scan of n <= 1024 ints in LDS by 1024 threads.
-__device__ void block_scan_incl(int* buf, int n) {
-  for (int off = 1; off < n; off <<= 1) {
-    int v = 0;
-    if (threadIdx.x < n && threadIdx.x >= off) v = buf[threadIdx.x - off];
-    __syncthreads();
-    if (threadIdx.x < n && threadIdx.x >= off) buf[threadIdx.x] += v;
-    __syncthreads();
+// Inclusive scans of a[0..n) and b[0..n) in LDS (n <= 1024) by the 1024-thread
+// group: each wave scans its 64 values by shuffles, wave 0 scans the 16 wave
+// totals, and every value takes the totals of the waves before it (integer
+// sums: the same results as any other order).  Two barriers, where a
+// Hillis-Steele scan of each array takes two per doubling.
+__device__ void block_scan2_incl(int* a, int* b, int n) {
+  __shared__ int wa[kPermWaves], wb[kPermWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = tid < n ? a[tid] : 0, y = tid < n ? b[tid] : 0;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int xo = __shfl_up(x, off), yo = __shfl_up(y, off);
+    if (lane >= off) {
+      x += xo;
+      y += yo;
+    }
   }
+  if (lane == 63) {
+    wa[w] = x;
+    wb[w] = y;
+  }
+  __syncthreads();
+  if (w == 0) {
+    int sx = lane < kPermWaves ? wa[lane] : 0, sy = lane < kPermWaves ? wb[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < kPermWaves; off <<= 1) {
+      const int xo = __shfl_up(sx, off), yo = __shfl_up(sy, off);
+      if (lane >= off) {
+        sx += xo;
+        sy += yo;
+      }
+    }
+    if (lane < kPermWaves) {
+      wa[lane] = sx;
+      wb[lane] = sy;
+    }
+  }
+  __syncthreads();
+  if (tid < n) {
+    a[tid] = x + (w > 0 ? wa[w - 1] : 0);
+    b[tid] = y + (w > 0 ? wb[w - 1] : 0);
+  }
+  __syncthreads();
 }
 
 // Single work-group: histogram, offsets, tile table, stable placement.
@@ -123,8 +183,7 @@ __device__ void permute_tables(const int* cnt, int* scan, int* tscan, int* curso
     tscan[tid] = (cnt[tid] + tile_m - 1) / tile_m;
   }
   __syncthreads();
-  block_scan_incl(scan, E);
-  block_scan_incl(tscan, E);
+  block_scan2_incl(scan, tscan, E);
   if (tid < E) {
     const int c = cnt[tid];
     const int off = scan[tid] - c;
@@ -197,17 +256,24 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
   __shared__ uint16_t wcnt[kPermWaves][kMaxE];
 
   const int tid = threadIdx.x;
-  for (int i = tid; i < kMaxE; i += kPermThreads) cnt[i] = 0;
-  for (int i = tid; i < kPermWaves * kMaxE; i += kPermThreads) (&wcnt[0][0])[i] = 0;
+  // The first chunk's ids are loaded once, before the tables, and kept for its
+  // placement.
+  const int e_first = tid < P ? ids[tid] : -1;
+  for (int i = tid; i < E; i += kPermThreads) {
+    cnt[i] = 0;
+#pragma unroll
+    for (int w = 0; w < kPermWaves; ++w) wcnt[w][i] = 0;
+  }
   __syncthreads();
-  for (int p = tid; p < P; p += kPermThreads) {
+  if (e_first >= 0 && e_first < E) atomicAdd(&cnt[e_first], 1);
+  for (int p = tid + kPermThreads; p < P; p += kPermThreads) {
     const int e = ids[p];
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
   permute_tables(cnt, scan, tscan, cursor, E, tile_m, counts, offsets, tiles, max_tiles, ntiles);
 
-  int e_next = (tid < P) ? ids[tid] : -1;
+  int e_next = e_first;
   for (int base = 0; base < P; base += kPermThreads) {
     const int p = base + tid;
     int e = e_next;
@@ -248,6 +314,11 @@ __global__ __launch_bounds__(256) void perm_hist_kernel(const int32_t* __restric
   for (int i = threadIdx.x; i < E; i += 256) hist[(size_t)blockIdx.x * E + i] = h[i];
 }
 
+// The per-chunk histograms become per-(chunk, expert) output bases.  G =
+// 1024 / E threads share an expert, each over a contiguous run of chunks: its
+// counts are loaded eight at a time (independent loads, one latency per batch
+// rather than one per chunk), summed, and, once the expert offsets are known,
+// loaded again (L2 hits) and overwritten with the running bases.
 __global__ __launch_bounds__(kPermThreads) void perm_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E,
                                                                  int tile_m, int32_t* __restrict__ counts,
                                                                  int32_t* __restrict__ offsets,
@@ -256,21 +327,47 @@ __global__ __launch_bounds__(kPermThreads) void perm_scan_kernel(int32_t* __rest
   __shared__ int cnt[kMaxE];
   __shared__ int scan[kMaxE];
   __shared__ int tscan[kMaxE];
-  const int e = threadIdx.x;
-  if (e < E) {
-    int run = 0;  // exclusive prefix over the chunks, per expert
-    for (int c = 0; c < nchunks; ++c) {
-      const int v = hist[(size_t)c * E + e];
-      hist[(size_t)c * E + e] = run;
-      run += v;
+  __shared__ int part[kPermThreads];  // part[g * E + e]: chunk run g's count of expert e
+  constexpr int B = 8;
+  const int tid = threadIdx.x;
+  const int G = kPermThreads / E;  // >= 1 (E <= 1024)
+  const int e = tid % E, g = tid / E;
+  const bool mine = g < G;
+  const int per = (nchunks + G - 1) / G;
+  const int c0 = min(nchunks, g * per), c1 = min(nchunks, c0 + per);
+  int local = 0;
+  if (mine) {
+    for (int c = c0; c < c1; c += B) {
+      int v[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) v[j] = c + j < c1 ? hist[(size_t)(c + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < B; ++j) local += v[j];
     }
-    cnt[e] = run;
+    part[tid] = local;
+  }
+  __syncthreads();
+  if (tid < E) {
+    int run = 0;
+    for (int gg = 0; gg < G; ++gg) run += part[gg * E + tid];
+    cnt[tid] = run;
   }
   __syncthreads();
   permute_tables(cnt, scan, tscan, nullptr, E, tile_m, counts, offsets, tiles, max_tiles, ntiles);
-  if (e < E) {
-    const int off = scan[e] - cnt[e];
-    for (int c = 0; c < nchunks; ++c) hist[(size_t)c * E + e] += off;
+  if (mine) {
+    int base = scan[e] - cnt[e];
+    for (int gg = 0; gg < g; ++gg) base += part[gg * E + e];
+    for (int c = c0; c < c1; c += B) {
+      int v[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) v[j] = c + j < c1 ? hist[(size_t)(c + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < B; ++j)
+        if (c + j < c1) {
+          hist[(size_t)(c + j) * E + e] = base;
+          base += v[j];
+        }
+    }
   }
 }
 
@@ -282,9 +379,11 @@ __global__ __launch_bounds__(kPermThreads) void perm_place_kernel(const int32_t*
   const int p = blockIdx.x * kPermThreads + threadIdx.x;
   int e = p < P ? ids[p] : -1;
   if (!(e >= 0 && e < E)) e = -1;
+  // the chunk's output base of this expert, requested before the ranking
+  const int b = e >= 0 ? base[(size_t)blockIdx.x * E + e] : 0;
   __syncthreads();
   const int rank = chunk_rank(e, wcnt);
-  if (e >= 0) sorted_pair[base[(size_t)blockIdx.x * E + e] + rank] = p;
+  if (e >= 0) sorted_pair[b + rank] = p;
 }
 
 }  // namespace ferret
@@ -297,8 +396,9 @@ extern "C" int ferret_moe_route_topk(const float* logits, int T, int E, int topk
   FERRET_REQUIRE(T >= 0 && E >= 1 && E <= kMaxE && topk >= 1 && topk <= kMaxTopk && topk <= E,
                  FERRET_ERR_SHAPE);
   if (T == 0) return FERRET_OK;
-  hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, logits, T, E,
-                     topk, ids, weights);
+  auto* kern = E <= 64 ? route_topk_kernel<1> : E <= 128 ? route_topk_kernel<2> : E <= 256 ? route_topk_kernel<4>
+             : E <= 512 ? route_topk_kernel<8> : route_topk_kernel<16>;
+  hipLaunchKernelGGL(kern, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, logits, T, E, topk, ids, weights);
   return (int)hipGetLastError();
 }
 
