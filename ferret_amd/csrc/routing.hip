@@ -214,32 +214,36 @@ __device__ void permute_tables(const int* cnt, int* scan, int* tscan, int* curso
 }
 
 // Stable rank of this thread's pair among the earlier pairs (lower thread
-// index) of the 1024-thread group with the same expert: within the wave from
-// ballots (one round per distinct expert), across waves from the per-wave
-// counts wcnt[w][e], which must be zero on entry and hold this chunk's counts
-// on return.  e = -1 marks an invalid pair (rank 0, not counted).
-__device__ int chunk_rank(int e, uint16_t (*wcnt)[kMaxE]) {
+// index) of the 1024-thread group with the same expert: within the wave, the
+// lanes holding the same expert are found by one ballot per bit of the expert
+// id (ebits of them, a fixed count instead of one round per distinct expert);
+// across waves from the per-wave counts wcnt[w][e], which must be zero on
+// entry and hold this chunk's counts on return.  e = -1 marks an invalid pair
+// (rank 0, not counted).
+__device__ int chunk_rank(int e, int ebits, uint16_t (*wcnt)[kMaxE]) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const bool valid = e >= 0;
+  uint64_t same = __ballot(valid);
+  for (int b = 0; b < ebits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t ones = __ballot(bit);
+    same &= bit ? ones : ~ones;
+  }
   int rank = 0;
-  uint64_t remaining = __ballot(valid);
-  while (remaining) {
-    const int leader = __ffsll((unsigned long long)remaining) - 1;  // wave-uniform
-    const int le = __builtin_amdgcn_readlane(e, leader);
-    const uint64_t m = __ballot(valid && e == le);
-    if (valid && e == le) {
-      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      rank = __popcll(m & lt);
-      if (lane == leader) wcnt[wave][e] = (uint16_t)__popcll(m);
-    }
-    remaining &= ~m;
+  if (valid) {
+    const uint64_t before = same & ((lane == 0) ? 0ull : (~0ull >> (64 - lane)));
+    rank = __popcll(before);
+    if (before == 0) wcnt[wave][e] = (uint16_t)__popcll(same);  // the expert's first lane in the wave
   }
   __syncthreads();
   if (valid)
     for (int w = 0; w < wave; ++w) rank += wcnt[w][e];
   return rank;
 }
+
+// Bits of an expert id below E (at least one).
+__device__ __forceinline__ int expert_bits(int E) { return 32 - __builtin_clz((unsigned)max(E - 1, 1)); }
 
 // Single work-group: histogram, tables, then stable placement chunk by chunk
 // in pair order (the next chunk's ids are loaded while one is placed).
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
     int e = e_next;
     e_next = (p + kPermThreads < P) ? ids[p + kPermThreads] : -1;
     if (!(e >= 0 && e < E)) e = -1;
-    const int rank = chunk_rank(e, wcnt);
+    const int rank = chunk_rank(e, expert_bits(E), wcnt);
     if (e >= 0) sorted_pair[cursor[e] + rank] = p;
     __syncthreads();
     if (tid < E) {
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(kPermThreads) void perm_place_kernel(const int32_t*
   // the chunk's output base of this expert, requested before the ranking
   const int b = e >= 0 ? base[(size_t)blockIdx.x * E + e] : 0;
   __syncthreads();
-  const int rank = chunk_rank(e, wcnt);
+  const int rank = chunk_rank(e, expert_bits(E), wcnt);
   if (e >= 0) sorted_pair[b + rank] = p;
 }
 
