@@ -42,25 +42,32 @@ __device__ __forceinline__ float from_order_bits(uint32_t h) {
 __device__ __forceinline__ bool key_gt(uint32_t h1, uint32_t l1, uint32_t h2, uint32_t l2) {
   return h1 > h2 || (h1 == h2 && l1 > l2);
 }
-// One step of a wave max over keys: each lane of the rows in ROWS takes the
-// larger of its key and that of the lane the DPP control names; lanes of the
-// other rows read their own key (the `old` operand) and keep it.
+// Wave maximum of an unsigned word by DPP: quad xor 1 and 2, half-row and row
+// mirror (each 16-lane row's maximum in all its lanes), then row broadcasts 15
+// (into rows 1 and 3) and 31 (into rows 2 and 3); lane 63 ends with the
+// maximum.  Lanes of rows a broadcast does not write keep their value (the
+// `old` operand).
 template <int CTRL, int ROWS = 0xF>
-__device__ __forceinline__ void key_max_dpp(uint32_t& h, uint32_t& l) {
-  const uint32_t ph = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROWS, 0xF, false);
-  const uint32_t pl = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROWS, 0xF, false);
-  if (key_gt(ph, pl, h, l)) {
-    h = ph;
-    l = pl;
-  }
+__device__ __forceinline__ uint32_t dpp_max_step(uint32_t x) {
+  const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROWS, 0xF, false);
+  return x > y ? x : y;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = dpp_max_step<0xB1>(x);        // quad_perm [1, 0, 3, 2]
+  x = dpp_max_step<0x4E>(x);        // quad_perm [2, 3, 0, 1]
+  x = dpp_max_step<0x141>(x);       // row_half_mirror
+  x = dpp_max_step<0x140>(x);       // row_mirror
+  x = dpp_max_step<0x142, 0xA>(x);  // row_bcast:15
+  x = dpp_max_step<0x143, 0xC>(x);  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
 
 // One wave per token; lane l owns experts l, l + 64, ... (PER slots, E <= 64 PER).
 // Each of the topk rounds takes the wave's largest untaken key: every lane
-// offers its best untaken slot, four DPP steps (quad xor 1, quad xor 2, half-row
-// mirror, row mirror) leave each 16-lane row's maximum in all of its lanes, two
-// row broadcasts carry the maximum to lane 63, and its key, read into scalar
-// registers, names the winner.  The owning lane marks the slot taken.  Weights: the full softmax over E at the
+// offers its best untaken slot, a DPP wave maximum of the first words names
+// the largest logit, the lane offering it gives the expert (a second DPP
+// maximum, over the second words of the lanes that tie, when the logit occurs
+// in several lanes), and the owning lane marks the slot taken.  Weights: the full softmax over E at the
 // chosen experts (not renormalised).
 template <int PER>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T, int E,
@@ -96,14 +103,15 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
         bh = kh[i];
         bl = kl[i];
       }
-    key_max_dpp<0xB1>(bh, bl);        // quad_perm [1, 0, 3, 2]
-    key_max_dpp<0x4E>(bh, bl);        // quad_perm [2, 3, 0, 1]
-    key_max_dpp<0x141>(bh, bl);       // row_half_mirror
-    key_max_dpp<0x140>(bh, bl);       // row_mirror: each row's maximum in all its lanes
-    key_max_dpp<0x142, 0xA>(bh, bl);  // row_bcast:15 into rows 1 and 3
-    key_max_dpp<0x143, 0xC>(bh, bl);  // row_bcast:31 into rows 2 and 3: lane 63 holds the maximum
-    const uint32_t wh = (uint32_t)__builtin_amdgcn_readlane((int)bh, 63);
-    const uint32_t wl = (uint32_t)__builtin_amdgcn_readlane((int)bl, 63);
+    // The largest first word; the lanes offering it; if several do (equal
+    // logits in different lanes), the largest second word among them.
+    const uint32_t wh = wave_max_u32(bh);
+    const uint64_t tie = __ballot(bh == wh);
+    uint32_t wl;
+    if (__popcll(tie) == 1)
+      wl = (uint32_t)__builtin_amdgcn_readlane((int)bl, __ffsll((unsigned long long)tie) - 1);
+    else
+      wl = wave_max_u32(bh == wh ? bl : 0u);
     const int sel = (int)~wl;
     if ((sel & 63) == lane) taken |= 1u << (sel >> 6);
     if (k == lane) {
