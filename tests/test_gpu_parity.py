@@ -297,6 +297,28 @@ def test_route_topk_bit_exact(ops, T, E, k):
     np.testing.assert_allclose(w.cpu().numpy(), ref_w, rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,k", [(256, 8), (384, 8), (64, 16), (1024, 16), (7, 7)])
+def test_route_topk_ties_across_lanes(ops, E, k):
+    """Rows whose top logits repeat in many lanes (the top-k's tie path: the
+    expert decides among equal logits), signed zeros (-0 ties +0), -inf and NaN
+    rows, against the stable argsort of the oracle."""
+    T = 6
+    lg = np.zeros((T, E), dtype=np.float32)
+    lg[0] = 1.0                                                   # every logit equal
+    lg[1] = np.where(np.arange(E) % 2 == 0, -0.0, 0.0)            # signed zeros only
+    lg[2] = np.where(np.arange(E) % 3 == 0, 2.0, -1.0)            # a third tied at the top
+    lg[3] = -np.inf
+    lg[3, E - 1] = np.nan                                         # -inf and NaN: index order
+    lg[4] = np.float32(np.nan)                                    # all NaN
+    lg[5] = np.round(np.random.default_rng(E).standard_normal(E), 0)  # few distinct values
+    logits = torch.from_numpy(lg).cuda()
+    ids, w = ops.moe_route_topk(logits, k)
+    torch.cuda.synchronize()
+    ref_ids, ref_w = R.route_topk(lg, k)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    np.testing.assert_allclose(w.cpu().numpy(), ref_w, rtol=1e-5, atol=1e-7)
+
+
 @pytest.mark.parametrize("T,k,E,tile_m,invalid", [(128, 8, 256, 16, False), (4096, 8, 256, 128, False),
                                                   (64, 8, 384, 16, False), (50, 3, 7, 4, True),
                                                   (1500, 2, 1024, 16, True), (1, 1, 1, 16, False)])
