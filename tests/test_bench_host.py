@@ -1,6 +1,7 @@
 """CPU checks of bench.py's host logic: the in-run traffic measurement stands
 down (returns None, starts no child process) where it cannot or must not run,
-the --gpus guard, and the committed traffic records the fallback reads."""
+the --gpus guard, the committed traffic records the fallback reads, and the
+correctness gate's handling of non-finite outputs."""
 import json
 import os
 import subprocess
@@ -78,3 +79,17 @@ def test_published_figures_name_existing_workloads_and_convert_to_their_unit():
     # GateUp M=16: 2 * 16 * 24576 * 4096 flops; the reference's kernel runs them at 62.91 TFLOP/s
     assert W.flops(W.WORKLOADS["qwen3_gateup_M16"]) == 2 * 16 * 24576 * 4096
     assert bench.published_of(W.WORKLOADS["dsv3_fp8_M4096"], R(), 100.0) is None
+
+
+def test_gate_rejects_non_finite_outputs():
+    """An all-NaN or partly-Inf output has no finite error to report (the
+    metric skips those elements), so the gate must fail it on the count."""
+    import numpy as np
+    from oracle import metrics as MT
+    ref = np.random.default_rng(0).standard_normal((8, 64)).astype(np.float32)
+    assert bench.passes_gate(*MT.fp8_rel_err(ref.copy(), ref))
+    for bad in (np.full_like(ref, np.nan), np.where(np.arange(ref.size).reshape(ref.shape) == 5, np.inf, ref)):
+        err, nbad = MT.fp8_rel_err(bad, ref)
+        assert nbad > 0 and err < 1e-2            # the error alone would pass
+        assert not bench.passes_gate(err, nbad)
+    assert not bench.passes_gate(*MT.fp8_rel_err(ref * 1.02, ref))
