@@ -345,7 +345,9 @@ def test_permute_bit_exact(ops, T, k, E, tile_m, invalid):
     assert not rt.tiles.cpu().numpy()[nt:].any()        # the table's tail is (0, 0, 0)
 
 
-@pytest.mark.parametrize("T,k,E,tile_m", [(3000, 8, 384, 16), (4096, 8, 256, 128), (2049, 1, 7, 128)])
+@pytest.mark.parametrize("T,k,E,tile_m", [(3000, 8, 384, 16), (4096, 8, 256, 128), (2049, 1, 7, 128),
+                                          (2500, 8, 1024, 16),     # one scan thread per expert, 20 chunks
+                                          (3000, 1, 1, 128)])      # 1024 scan threads on one expert
 def test_permute_multi_group_matches_single_group(hip, ops, T, k, E, tile_m):
     """The multi-work-group path (workspace given) and the one-group path (NULL) agree bit for bit."""
     rng = np.random.default_rng(T * k + E)
