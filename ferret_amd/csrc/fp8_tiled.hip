@@ -523,11 +523,9 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
     // split-K: fp32 partials.  As for the bf16 store, the idle ring stages the
     // wave's TOKW x 64 sub-tile (pitch 272 B: the 16 rows of one write land on
     // distinct banks), so that each store writes four whole 256-B row segments
-    // instead of 64-B quarters of 16 rows.  The stores are non-temporal: the
-    // 16.8 MB of partials at M = 128, N = 4096 then leave the L2 as they are
-    // written instead of waiting dirty for the write-back at the kernel's end
-    // (20.05 -> 19.47 us with the reduce; non-temporal loads in the reduce
-    // changed nothing).
+    // instead of 64-B quarters of 16 rows.  (Non-temporal partial stores were
+    // 3 % faster back to back but 6 % slower after the reference's write
+    // flush, which leaves the caches full of dirty lines; they stay cached.)
     if (nb * TB_N + wn * 64 >= N) return;  // wave's rows lie past N
     constexpr int PITCH = 272;
     static_assert(TB_WAVES * TOKW * PITCH <= C::kLds, "staging fits the ring");
@@ -545,8 +543,8 @@ __global__ __launch_bounds__(64 * WN * TW) void fp8_tiled_kernel(TiledArgs p) {
       const int tl = wm * TOKW + rw;  // token row inside the tile
       const f32x4 v = *reinterpret_cast<const f32x4*>(stg + rw * PITCH + chunk * 16);
       if (tl < nrows)
-        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N +
-                                                                 nb * TB_N + wn * 64 + chunk * 4));
+        *reinterpret_cast<f32x4*>(p.partial + ((size_t)blockIdx.y * p.M + row0 + tl) * N + nb * TB_N + wn * 64 +
+                                  chunk * 4) = v;
     }
   }
 }
