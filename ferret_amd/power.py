@@ -4,8 +4,10 @@
 
 SPEC is a workload key (ferret_amd.workloads.WORKLOADS), optionally followed by
 `:full` or `:partial` for a grouped MoE GEMM (only the tiles of the routing's
-tile table with tile_m rows, or only those with fewer), or
-`torch.matmul:MxNxK` for the vendor bf16 GEMM of that shape.  Each SPEC runs
+tile table with tile_m rows, or only those with fewer), or by `:full|partial`
+(both subsets launched together on two streams of default priority, each
+step waiting for both), or `torch.matmul:MxNxK` for the vendor bf16 GEMM of
+that shape.  Each SPEC runs
 back to back for S seconds; the table gives the time per launch, the board's
 average power over the run (the first fifth, the ramp, left out), the idle
 power just before, and the energy per launch.
@@ -143,22 +145,44 @@ def _launcher(spec: str):
     inp = W.make_inputs(wl, "cuda")
     if wl.kind in ("moe_fp8", "moe_fp8_w2", "moe_w4a16"):
         ids, _ = ops.moe_route_topk(inp["logits"], wl.topk)
-        rt = ops.moe_permute(ids, wl.E)
-        if arg:
-            nt = int(rt.ntiles.item())
-            sel = tile_subset(rt.tiles.cpu(), nt, rt.tile_m, arg)
-            tiles = torch.zeros_like(rt.tiles)
-            tiles[: sel.shape[0]] = sel.to(tiles.device)
-            rt = dataclasses.replace(rt, tiles=tiles,
-                                     ntiles=torch.tensor([sel.shape[0]], dtype=torch.int32, device="cuda"))
+        rt_all = ops.moe_permute(ids, wl.E)
         cols = wl.N if wl.kind == "moe_fp8_w2" else wl.N // 2
-        out = torch.empty((wl.T * wl.topk, cols), dtype=torch.bfloat16, device="cuda")
-        if wl.kind == "moe_fp8":
-            return lambda: ops.moe_w13_fp8(inp["x"], inp["sx"], inp["w"], inp["sw"], rt, out=out)
-        if wl.kind == "moe_fp8_w2":
-            return lambda: ops.moe_w2_fp8(inp["h"], inp["sh"], inp["w"], inp["sw"], rt, out=out)
-        wt = ops.int4_tile_weights(inp["w"])
-        return lambda: ops.moe_w13_w4a16(inp["x"], wt, inp["ws"], rt, out=out)
+        wt = ops.int4_tile_weights(inp["w"]) if wl.kind == "moe_w4a16" else None
+
+        def one(which):
+            rt = rt_all
+            if which:
+                nt = int(rt.ntiles.item())
+                sel = tile_subset(rt.tiles.cpu(), nt, rt.tile_m, which)
+                tiles = torch.zeros_like(rt.tiles)
+                tiles[: sel.shape[0]] = sel.to(tiles.device)
+                rt = dataclasses.replace(rt, tiles=tiles,
+                                         ntiles=torch.tensor([sel.shape[0]], dtype=torch.int32, device="cuda"))
+            out = torch.empty((wl.T * wl.topk, cols), dtype=torch.bfloat16, device="cuda")
+            if wl.kind == "moe_fp8":
+                return lambda: ops.moe_w13_fp8(inp["x"], inp["sx"], inp["w"], inp["sw"], rt, out=out)
+            if wl.kind == "moe_fp8_w2":
+                return lambda: ops.moe_w2_fp8(inp["h"], inp["sh"], inp["w"], inp["sw"], rt, out=out)
+            return lambda: ops.moe_w13_w4a16(inp["x"], wt, inp["ws"], rt, out=out)
+
+        if "|" not in arg:
+            return one(arg)
+        # Both tile classes at once: each on its own stream (default priority),
+        # the caller's stream waiting for both.
+        fa, fb = (one(w) for w in arg.split("|"))
+        sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+
+        def both():
+            cur = torch.cuda.current_stream()
+            sa.wait_stream(cur)
+            sb.wait_stream(cur)
+            with torch.cuda.stream(sa):
+                fa()
+            with torch.cuda.stream(sb):
+                fb()
+            cur.wait_stream(sa)
+            cur.wait_stream(sb)
+        return both
     if arg:
         raise ValueError(f"{spec}: a tile class applies to grouped MoE workloads only")
     out = torch.empty((wl.M, wl.N), dtype=torch.bfloat16, device="cuda")
